@@ -1,0 +1,526 @@
+// Flash attention forward on gfx950 MFMA.
+//
+// Replaces fused_attention_forward (reference csrc/attention_dispatch.cuh:332-519)
+// and the tensor-core kernel behind it (reference csrc/attention_wmma.cuh:874-1770):
+// softmax(Q K^T * scale  (+ causal / key mask)) V with fp16 operands and fp32
+// accumulation and softmax, online (the S x S matrix never exists), a query
+// row with no allowed key giving 0, output written straight into either
+// [B, H, S, hd] or the [B, S, H*hd] layout out_proj consumes.
+//
+// MI355X design (not the reference's warp-shaped one):
+//   * the score tile is computed TRANSPOSED, S^T = K Q^T, with
+//     v_mfma_f32_32x32x16_f16: K is the A operand (32 keys x 16 hd, one
+//     16-byte LDS read per lane), Q^T the B operand (held in registers for
+//     the whole key loop). In the 32x32 accumulator lane l then owns ONE
+//     query (column l%32) and 16 keys, so the running max and the exponent
+//     sums are in-lane; only one exchange with lane l^32 per key tile is
+//     needed to finish a row maximum -- no quad shuffles per score;
+//   * the probabilities never leave registers: the PV product is also
+//     transposed, O^T += V^T P^T, and P^T's B-operand layout (lane l: query
+//     l%32, 8 keys of lane group l/32) is exactly the score accumulator's
+//     layout, so the fp32 -> fp16 narrowing of P is the only work between
+//     the two matrix products. The key order inside each 16-key MFMA step is
+//     permuted to match (a contraction does not care), and V is fetched in
+//     the same permuted order;
+//   * V is transposed while it is staged into LDS ([hd][keys]), two keys per
+//     32-bit LDS write, so each V^T fragment is two 8-byte LDS reads;
+//   * one wavefront per 32 queries, NW wavefronts per workgroup sharing one
+//     K/V tile of 64 keys; the next tile's K/V are fetched from HBM into
+//     registers while the current tile is multiplied (register double
+//     buffering);
+//   * causal: key tiles past the workgroup's last query are never visited,
+//     and a wavefront skips the arithmetic of tiles wholly in its future;
+//     workgroups are numbered so the heaviest (latest) query blocks of every
+//     head are dispatched first;
+//   * key-only masks ([B,1,1,S] broadcast, the padded-batch case): a tile
+//     whose 64 keys are all masked is skipped outright, decided identically
+//     by every wavefront from a ballot, so no barrier is needed;
+//   * all mask/causal/bounds tests are compiled into a slow path taken only
+//     by tiles that need it (boundary, diagonal, or masked tiles).
+#include "dotl_common.h"
+
+namespace dotl {
+
+int attention_fp16_default();
+
+namespace {
+
+constexpr int kBN = 64;    // keys per tile
+constexpr int kVPad = 8;   // halves of padding per V^T row
+constexpr int kKPad = 8;   // halves of padding per K row
+
+template <bool IN_F32>
+struct Elem;
+template <>
+struct Elem<false> { using T = _Float16; };
+template <>
+struct Elem<true> { using T = float; };
+
+// Load 8 consecutive head-dim elements as fp16 (narrowing fp32 with RNE).
+template <bool IN_F32>
+__device__ __forceinline__ half8 load8(const typename Elem<IN_F32>::T* p) {
+    if constexpr (IN_F32) {
+        const float4 a = *reinterpret_cast<const float4*>(p);
+        const float4 b = *reinterpret_cast<const float4*>(p + 4);
+        half8 h;
+        h[0] = to_half(a.x); h[1] = to_half(a.y); h[2] = to_half(a.z); h[3] = to_half(a.w);
+        h[4] = to_half(b.x); h[5] = to_half(b.y); h[6] = to_half(b.z); h[7] = to_half(b.w);
+        return h;
+    } else {
+        return *reinterpret_cast<const half8*>(p);
+    }
+}
+
+struct AttnParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    int64_t sb, sh, ss;          // q/k/v strides (elements): batch, head, seq
+    const uint8_t* mask;         // nullable
+    int64_t mb, mh, mq, mk;      // mask strides (elements)
+    void* out;
+    int out_layout;              // 0 [B,H,S,hd], 1 [B,S,H*hd]
+    int B, H, S;
+    int nqb;                     // query blocks per (b, h)
+    int causal;
+    float scale_log2;            // scale * log2(e)
+};
+
+template <int HD, int NW, bool IN_F32, bool OUT_F32>
+__global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
+    using T = typename Elem<IN_F32>::T;
+    constexpr int NT = NW * 64;
+    constexpr int BM = NW * 32;
+    constexpr int KS = HD / 16;          // k-steps of the score product
+    constexpr int HT = HD / 32;          // 32-row hd tiles of O^T
+    constexpr int LDK = HD + kKPad;      // K row pitch (halves)
+    constexpr int LDV = kBN + kVPad;     // V^T row pitch (halves)
+
+    __shared__ __attribute__((aligned(16))) _Float16 sK[kBN * LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 sVt[HD * LDV];
+    __shared__ uint8_t sMask[kBN];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int lr = lane & 31;
+    const int lg = lane >> 5;
+
+    // Block numbering: the query-block index is the slowest-varying part so
+    // that, under causal masking, the longest blocks of every (b, h) come first.
+    const int bh_count = p.B * p.H;
+    const int id = blockIdx.x;
+    int qb = id / bh_count;
+    const int bh = id - qb * bh_count;
+    if (p.causal) qb = p.nqb - 1 - qb;
+    const int b = bh / p.H;
+    const int h = bh - b * p.H;
+
+    const int q_wg0 = qb * BM;
+    const int q_w0 = q_wg0 + wave * 32;   // this wavefront's first query
+    const int my_q = q_w0 + lr;           // the query this lane's column is
+
+    const T* qbase = static_cast<const T*>(p.q) + b * p.sb + h * p.sh;
+    const T* kbase = static_cast<const T*>(p.k) + b * p.sb + h * p.sh;
+    const T* vbase = static_cast<const T*>(p.v) + b * p.sb + h * p.sh;
+
+    // Q^T fragments for the whole key loop: lane supplies Q[my_q][ks*16 + lg*8 .. +8].
+    half8 qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        qf[ks] = half8{};
+        if (my_q < p.S) qf[ks] = load8<IN_F32>(qbase + static_cast<int64_t>(my_q) * p.ss + ks * 16 + lg * 8);
+    }
+
+    const bool has_mask = p.mask != nullptr;
+    const bool key_only_mask = has_mask && p.mq == 0;
+    const uint8_t* mbase = has_mask ? p.mask + b * p.mb + h * p.mh : nullptr;
+
+    // Key range this workgroup visits.
+    int kend = p.S;
+    if (p.causal) kend = min(p.S, q_wg0 + BM);
+    const int nkt = (kend + kBN - 1) / kBN;
+
+    // Live-tile test for a key-only mask: any allowed key in the tile.
+    auto tile_live = [&](int kt) -> bool {
+        if (!key_only_mask) return true;
+        const int key = kt * kBN + lane;
+        const bool ok = key < p.S && mbase[static_cast<int64_t>(key) * p.mk] != 0;
+        return __ballot(ok) != 0ull;
+    };
+
+    // Staging registers. K: HD/8 chunks per key row, 64 rows.
+    constexpr int KCH = kBN * HD / 8;
+    constexpr int KPER = (KCH + NT - 1) / NT;
+    // V: items are (key pair, 8-wide hd chunk): 32 * HD/8 of them.
+    constexpr int VIT = 32 * HD / 8;
+    constexpr int VPER = (VIT + NT - 1) / NT;
+    half8 rk[KPER];
+    half8 rv0[VPER], rv1[VPER];
+    uint8_t rm = 0;
+
+    auto fetch = [&](int kt) {
+        const int key0 = kt * kBN;
+#pragma unroll
+        for (int i = 0; i < KPER; ++i) {
+            const int c = threadIdx.x + i * NT;
+            const int row = c / (HD / 8);
+            const int col = (c % (HD / 8)) * 8;
+            rk[i] = half8{};
+            if (c < KCH && key0 + row < p.S)
+                rk[i] = load8<IN_F32>(kbase + static_cast<int64_t>(key0 + row) * p.ss + col);
+        }
+#pragma unroll
+        for (int i = 0; i < VPER; ++i) {
+            const int it = threadIdx.x + i * NT;
+            const int kp = it & 31;          // key pair
+            const int ch = it >> 5;          // hd chunk
+            rv0[i] = half8{};
+            rv1[i] = half8{};
+            if (it < VIT) {
+                const int k0 = key0 + 2 * kp;
+                if (k0 < p.S) rv0[i] = load8<IN_F32>(vbase + static_cast<int64_t>(k0) * p.ss + ch * 8);
+                if (k0 + 1 < p.S) rv1[i] = load8<IN_F32>(vbase + static_cast<int64_t>(k0 + 1) * p.ss + ch * 8);
+            }
+        }
+        if (key_only_mask && threadIdx.x < kBN) {
+            const int key = key0 + threadIdx.x;
+            rm = (key < p.S) ? mbase[static_cast<int64_t>(key) * p.mk] : 0;
+        }
+    };
+
+    auto commit = [&]() {
+#pragma unroll
+        for (int i = 0; i < KPER; ++i) {
+            const int c = threadIdx.x + i * NT;
+            if (c < KCH) {
+                const int row = c / (HD / 8);
+                const int col = (c % (HD / 8)) * 8;
+                *reinterpret_cast<half8*>(sK + row * LDK + col) = rk[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VPER; ++i) {
+            const int it = threadIdx.x + i * NT;
+            if (it < VIT) {
+                const int kp = it & 31;
+                const int ch = it >> 5;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    half2v pair;
+                    pair[0] = rv0[i][e];
+                    pair[1] = rv1[i][e];
+                    *reinterpret_cast<half2v*>(sVt + (ch * 8 + e) * LDV + 2 * kp) = pair;
+                }
+            }
+        }
+        if (key_only_mask && threadIdx.x < kBN) sMask[threadIdx.x] = rm;
+    };
+
+    floatx16 o[HT];
+#pragma unroll
+    for (int j = 0; j < HT; ++j) o[j] = floatx16{};
+    float m_run = -INFINITY;   // running max (scaled log2 domain) of this lane's query
+    float l_run = 0.f;         // this lane's share of the exponent sum
+
+    // First live tile.
+    int kt = 0;
+    while (kt < nkt && !tile_live(kt)) ++kt;
+    if (kt < nkt) fetch(kt);
+
+    while (kt < nkt) {
+        int nxt = kt + 1;
+        while (nxt < nkt && !tile_live(nxt)) ++nxt;
+
+        __syncthreads();
+        commit();
+        __syncthreads();
+        if (nxt < nkt) fetch(nxt);
+
+        const int key0 = kt * kBN;
+        // A wavefront whose queries all precede this tile has nothing to add.
+        const bool wave_active = !p.causal || key0 <= q_w0 + 31;
+        if (wave_active) {
+            floatx16 s[2];
+            s[0] = floatx16{};
+            s[1] = floatx16{};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+                for (int t2 = 0; t2 < 2; ++t2) {
+                    const half8 kf = *reinterpret_cast<const half8*>(sK + (t2 * 32 + lr) * LDK + ks * 16 + lg * 8);
+                    s[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[t2], 0, 0, 0);
+                }
+            }
+
+            // Scale into the log2 domain, then mask where this tile needs it.
+            const bool full = key0 + kBN <= p.S;
+            const bool diag = p.causal && key0 + kBN - 1 > q_w0;
+            const bool needs_test = !full || diag || has_mask;
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float x = s[t2][r] * p.scale_log2;
+                    if (needs_test) {
+                        const int kl = t2 * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+                        const int key = key0 + kl;
+                        bool ok = key < p.S;
+                        if (p.causal) ok = ok && key <= my_q;
+                        if (has_mask) {
+                            if (key_only_mask) {
+                                ok = ok && sMask[kl] != 0;
+                            } else if (ok && my_q < p.S) {
+                                ok = mbase[static_cast<int64_t>(my_q) * p.mq +
+                                           static_cast<int64_t>(key) * p.mk] != 0;
+                            }
+                        }
+                        if (!ok) x = -INFINITY;
+                    }
+                    s[t2][r] = x;
+                    tmax = fmaxf(tmax, x);
+                }
+            }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+            const float m_new = fmaxf(m_run, tmax);
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+            m_run = m_new;
+
+            float lsum = 0.f;
+            half8 pf[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float pv = __builtin_amdgcn_exp2f(s[t >> 1][8 * (t & 1) + e] - m_use);
+                    lsum += pv;
+                    pf[t][e] = to_half(pv);
+                }
+            }
+            l_run = l_run * corr + lsum;
+#pragma unroll
+            for (int j = 0; j < HT; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[j][r] *= corr;
+
+            // O^T[hd, q] += V^T[hd, keys] P^T[keys, q]. Key order within MFMA
+            // step t: element e of lane group g is key
+            // 32*(t/2) + 16*(t%2) + 8*(e/4) + 4*g + e%4.
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int kb = 32 * (t >> 1) + 16 * (t & 1) + 4 * lg;
+#pragma unroll
+                for (int j = 0; j < HT; ++j) {
+                    const _Float16* vrow = sVt + (j * 32 + lr) * LDV + kb;
+                    const half4 lo = *reinterpret_cast<const half4*>(vrow);
+                    const half4 hi = *reinterpret_cast<const half4*>(vrow + 8);
+                    half8 vf;
+                    vf[0] = lo[0]; vf[1] = lo[1]; vf[2] = lo[2]; vf[3] = lo[3];
+                    vf[4] = hi[0]; vf[5] = hi[1]; vf[6] = hi[2]; vf[7] = hi[3];
+                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], o[j], 0, 0, 0);
+                }
+            }
+        }
+        kt = nxt;
+    }
+
+    // Normalise and store. O^T register r of tile j at lane l: hd row
+    // 32*j + 8*(r/4) + 4*g + r%4, query column l%32.
+    const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    if (my_q < p.S) {
+        const int64_t obase =
+            p.out_layout == 1
+                ? ((static_cast<int64_t>(b) * p.S + my_q) * p.H + h) * HD
+                : ((static_cast<int64_t>(b) * p.H + h) * p.S + my_q) * HD;
+#pragma unroll
+        for (int j = 0; j < HT; ++j) {
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const int d = 32 * j + 8 * rb + 4 * lg;
+                if constexpr (OUT_F32) {
+                    float4 w4 = make_float4(o[j][4 * rb] * inv, o[j][4 * rb + 1] * inv,
+                                            o[j][4 * rb + 2] * inv, o[j][4 * rb + 3] * inv);
+                    *reinterpret_cast<float4*>(static_cast<float*>(p.out) + obase + d) = w4;
+                } else {
+                    half4 w4;
+                    w4[0] = to_half(o[j][4 * rb] * inv);
+                    w4[1] = to_half(o[j][4 * rb + 1] * inv);
+                    w4[2] = to_half(o[j][4 * rb + 2] * inv);
+                    w4[3] = to_half(o[j][4 * rb + 3] * inv);
+                    *reinterpret_cast<half4*>(static_cast<_Float16*>(p.out) + obase + d) = w4;
+                }
+            }
+        }
+    }
+}
+
+template <int HD, int NW, bool IN_F32, bool OUT_F32>
+void launch_attn(const AttnParams& p, hipStream_t stream) {
+    const int64_t blocks = static_cast<int64_t>(p.nqb) * p.B * p.H;
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, IN_F32, OUT_F32>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(NW * 64), 0, stream, p);
+}
+
+// Wavefronts per workgroup: enough to cover short sequences without idle
+// waves, 4 otherwise. p.nqb must already be query_blocks(S).
+int waves_for(int S) { return S <= 32 ? 1 : (S <= 64 ? 2 : 4); }
+int query_blocks(int S) { return (S + 32 * waves_for(S) - 1) / (32 * waves_for(S)); }
+
+template <int HD, bool IN_F32, bool OUT_F32>
+void launch_nw(const AttnParams& p, hipStream_t stream) {
+    switch (waves_for(p.S)) {
+        case 1: launch_attn<HD, 1, IN_F32, OUT_F32>(p, stream); break;
+        case 2: launch_attn<HD, 2, IN_F32, OUT_F32>(p, stream); break;
+        default: launch_attn<HD, 4, IN_F32, OUT_F32>(p, stream); break;
+    }
+}
+
+template <bool IN_F32, bool OUT_F32>
+bool launch_hd(int hd, const AttnParams& p, hipStream_t stream) {
+    switch (hd) {
+        case 32: launch_nw<32, IN_F32, OUT_F32>(p, stream); return true;
+        case 64: launch_nw<64, IN_F32, OUT_F32>(p, stream); return true;
+        case 128: launch_nw<128, IN_F32, OUT_F32>(p, stream); return true;
+        default: return false;
+    }
+}
+
+const char* impl_name(int impl) {
+    switch (impl) {
+        case 0: return "auto";
+        case 1: return "scalar";
+        case 2: return "wmma";
+        case 3: return "tile";
+    }
+    return "?";
+}
+
+const char* precision_name(int prec) {
+    switch (prec) {
+        case 0: return "auto";
+        case 1: return "fp32";
+        case 2: return "tf32";
+        case 3: return "fp16";
+        case 4: return "bf16";
+    }
+    return "?";
+}
+
+}  // namespace
+}  // namespace dotl
+
+extern "C" int dotl_attention_forward(const void* q, const void* k, const void* v, int dtype,
+                                      const int64_t* qkv_strides, const uint8_t* mask,
+                                      const int64_t* mask_strides, void* out, int out_dtype,
+                                      int out_layout, int B, int H, int S, int head_dim,
+                                      int is_causal, double scale, int impl, int precision,
+                                      void* stream) {
+    using namespace dotl;
+    clear_error();
+    DOTL_REQUIRE(out_layout == 0 || out_layout == 1,
+                 "fused_attention_forward: out_layout must be 0 ([B,H,S,head_dim]) or 1 "
+                 "([B,S,H*head_dim])");
+    DOTL_REQUIRE(impl >= 0 && impl <= 3,
+                 "fused_attention_forward: impl must be 0 (auto), 1 (scalar), 2 (wmma) or 3 (tile)");
+    DOTL_REQUIRE(precision >= 0 && precision <= 4,
+                 "fused_attention_forward: precision must be 0 (auto), 1 (fp32), 2 (tf32), "
+                 "3 (fp16) or 4 (bf16)");
+    DOTL_REQUIRE(dtype == DOTL_F16 || dtype == DOTL_F32,
+                 "fused_attention_forward: q/k/v must be float16 or float32");
+    DOTL_REQUIRE(out_dtype == DOTL_F16 || out_dtype == DOTL_F32,
+                 "fused_attention_forward: out must be float16 or float32");
+    DOTL_REQUIRE(B >= 0 && H >= 0 && S >= 0 && head_dim > 0,
+                 "fused_attention_forward: negative extent");
+    DOTL_REQUIRE(qkv_strides != nullptr, "fused_attention_forward: strides required");
+
+    // The impl x precision vocabulary of the reference
+    // (reference csrc/attention_dispatch.cuh:221-304): a forced impl asking for
+    // arithmetic it does not have is an error; "tile" is an NVIDIA programming
+    // model with no counterpart here and always reports unavailable.
+    if (impl == 3) {
+        set_error("fused_attention_forward: impl=3 (tile) is not available in this build: the "
+                  "tile programming model has no gfx950 counterpart");
+        return DOTL_E_UNSUPPORTED;
+    }
+    int prec = precision;
+    if (prec == 0) prec = attention_fp16_default() ? 3 : 1;
+    if (impl == 2 && prec == 1) {
+        set_error("fused_attention_forward: --attn-impl wmma has no fp32 arithmetic. It supports: "
+                  "fp16. Note this is the MATH type, not the tensor dtype.");
+        return DOTL_E_UNSUPPORTED;
+    }
+    if (impl == 1 && precision != 0 && precision != 1) {
+        set_error(std::string("fused_attention_forward: --attn-impl scalar has no ") +
+                  precision_name(precision) + " arithmetic. It supports: fp32.");
+        return DOTL_E_UNSUPPORTED;
+    }
+    if (prec != 3 || impl == 1) {
+        char buf[256];
+        std::snprintf(buf, sizeof(buf),
+                      "fused_attention_forward: impl=%d (%s), precision=%s is not covered by this "
+                      "build: the MFMA kernel contracts in fp16",
+                      impl, impl_name(impl), precision_name(prec));
+        set_error(buf);
+        return DOTL_DECLINED;
+    }
+    if (B == 0 || H == 0 || S == 0) return DOTL_OK;
+    DOTL_REQUIRE(q && k && v && out, "fused_attention_forward: null pointer");
+    DOTL_REQUIRE(mask == nullptr || mask_strides != nullptr,
+                 "fused_attention_forward: mask strides required with a mask");
+    const int64_t es = dtype == DOTL_F16 ? 2 : 4;
+    const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                            reinterpret_cast<uintptr_t>(v) |
+                            static_cast<uintptr_t>(qkv_strides[0] * es) |
+                            static_cast<uintptr_t>(qkv_strides[1] * es) |
+                            static_cast<uintptr_t>(qkv_strides[2] * es);
+    DOTL_REQUIRE(align % 16 == 0,
+                 "fused_attention_forward: q/k/v rows must be 16-byte aligned");
+
+    AttnParams p{};
+    p.q = q; p.k = k; p.v = v;
+    p.sb = qkv_strides[0]; p.sh = qkv_strides[1]; p.ss = qkv_strides[2];
+    p.mask = mask;
+    if (mask) {
+        p.mb = mask_strides[0]; p.mh = mask_strides[1];
+        p.mq = mask_strides[2]; p.mk = mask_strides[3];
+    }
+    p.out = out;
+    p.out_layout = out_layout;
+    p.B = B; p.H = H; p.S = S;
+    p.causal = is_causal ? 1 : 0;
+    p.nqb = query_blocks(S);
+    DOTL_REQUIRE(static_cast<int64_t>(p.nqb) * B * H <= 0x7fffffff,
+                 "fused_attention_forward: grid too large");
+    p.scale_log2 = static_cast<float>(scale * 1.4426950408889634);
+    const hipStream_t st = as_stream(stream);
+
+    bool launched;
+    const bool in32 = dtype == DOTL_F32;
+    const bool out32 = out_dtype == DOTL_F32;
+    if (in32) {
+        launched = out32 ? launch_hd<true, true>(head_dim, p, st) : launch_hd<true, false>(head_dim, p, st);
+    } else {
+        launched = out32 ? launch_hd<false, true>(head_dim, p, st) : launch_hd<false, false>(head_dim, p, st);
+    }
+    if (!launched) {
+        char buf[256];
+        std::snprintf(buf, sizeof(buf),
+                      "fused_attention_forward: impl=%d (%s), precision=%s does not cover "
+                      "head_dim=%d; the MFMA kernel covers head_dim in {32, 64, 128}",
+                      impl, impl_name(impl), precision_name(prec), head_dim);
+        set_error(buf);
+        return DOTL_DECLINED;
+    }
+    return check_launch("fused_attention_forward");
+}
+
+extern "C" int dotl_ffn_block(const float*, const float*, const float*, const float*,
+                              const float*, const float*, const float*, const float*,
+                              const float*, const float*, float*, float*, int64_t, int64_t,
+                              int64_t, double, void*) {
+    dotl::clear_error();
+    dotl::set_error("fused_ffn_block: no fused block in this build; run the unfused chain");
+    return DOTL_DECLINED;
+}

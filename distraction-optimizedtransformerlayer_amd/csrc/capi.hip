@@ -1,0 +1,123 @@
+// Library-wide C-ABI entries: error channel, version, knobs, the build smoke
+// test and the MFMA accumulator-layout probe.
+#include "dotl_common.h"
+
+#include <atomic>
+
+namespace dotl {
+
+namespace {
+thread_local std::string g_last_error;
+std::atomic<int> g_wmma_fp16{1};
+std::atomic<int> g_cp_async{2};
+}  // namespace
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+void clear_error() { g_last_error.clear(); }
+
+int check_launch(const char* who) {
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        set_error(std::string(who) + ": kernel launch failed: " + hipGetErrorString(err));
+        return DOTL_E_LAUNCH;
+    }
+    return DOTL_OK;
+}
+
+int attention_fp16_default() { return g_wmma_fp16.load(std::memory_order_relaxed); }
+
+namespace {
+
+__global__ void identity_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = x[i];
+}
+
+// One wavefront. Operand A row i carries a one-hot of i across k, operand B
+// column j carries (j + 1) at k == that one-hot: C[i][j] = (j + 1) * [k match].
+// Chosen so each accumulator element encodes its own (row, col):
+//   A[i][k] = (k == i % K) ? 1 : 0 ... not unique for rows >= K, so instead
+// the probe runs the MFMA with A[i][k] = i + 1 at k == 0 only and
+// B[k][j] = 1 at k == 0 only, giving C[i][j] = i + 1, then a second MFMA with
+// A[i][0] = 1 and B[0][j] = j + 1, giving C[i][j] = j + 1. Both are exact in
+// fp16/fp32 for i, j < 32.
+__global__ void mfma_probe_kernel(int32_t* out) {
+    const int lane = threadIdx.x;
+    // 32x32x16: lane supplies A[l % 32][8 * (l / 32) + e] and B[8 * (l / 32) + e][l % 32].
+    {
+        half8 a_row = {}, b_one = {}, a_one = {}, b_col = {};
+        if (lane < 32) {  // k == 0 lives in lane group 0, element 0
+            a_row[0] = static_cast<_Float16>(lane % 32 + 1);
+            b_one[0] = static_cast<_Float16>(1.0f);
+            a_one[0] = static_cast<_Float16>(1.0f);
+            b_col[0] = static_cast<_Float16>(lane % 32 + 1);
+        }
+        floatx16 zero = {};
+        floatx16 rows = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_row, b_one, zero, 0, 0, 0);
+        floatx16 cols = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_one, b_col, zero, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = static_cast<int>(rows[r]) - 1;
+            const int col = static_cast<int>(cols[r]) - 1;
+            out[lane * 16 + r] = row * 32 + col;
+        }
+    }
+    // 16x16x32: lane supplies A[l % 16][8 * (l / 16) + e] and B[8 * (l / 16) + e][l % 16].
+    {
+        half8 a_row = {}, b_one = {}, a_one = {}, b_col = {};
+        if (lane < 16) {
+            a_row[0] = static_cast<_Float16>(lane % 16 + 1);
+            b_one[0] = static_cast<_Float16>(1.0f);
+            a_one[0] = static_cast<_Float16>(1.0f);
+            b_col[0] = static_cast<_Float16>(lane % 16 + 1);
+        }
+        floatx4 zero = {};
+        floatx4 rows = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_row, b_one, zero, 0, 0, 0);
+        floatx4 cols = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_one, b_col, zero, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = static_cast<int>(rows[r]) - 1;
+            const int col = static_cast<int>(cols[r]) - 1;
+            out[1024 + lane * 4 + r] = row * 16 + col;
+        }
+    }
+}
+
+}  // namespace
+}  // namespace dotl
+
+extern "C" {
+
+const char* dotl_last_error(void) { return dotl::g_last_error.c_str(); }
+
+int dotl_abi_version(void) { return DOTL_ABI_VERSION; }
+
+const char* dotl_target(void) { return "gfx950"; }
+
+int dotl_smoke_test_identity(const float* x, float* y, int64_t n, void* stream) {
+    dotl::clear_error();
+    DOTL_REQUIRE(n >= 0, "smoke_test_identity: n must be non-negative, got %lld",
+                 static_cast<long long>(n));
+    if (n == 0) return DOTL_OK;
+    DOTL_REQUIRE(x != nullptr && y != nullptr, "smoke_test_identity: null pointer");
+    const int threads = 256;
+    const int64_t blocks = (n + threads - 1) / threads;
+    DOTL_REQUIRE(blocks <= 0x7fffffff, "smoke_test_identity: n too large");
+    hipLaunchKernelGGL(dotl::identity_kernel, dim3(static_cast<unsigned>(blocks)), dim3(threads),
+                       0, dotl::as_stream(stream), x, y, n);
+    return dotl::check_launch("smoke_test_identity");
+}
+
+int dotl_mfma_layout_probe(int32_t* out, void* stream) {
+    dotl::clear_error();
+    DOTL_REQUIRE(out != nullptr, "mfma_layout_probe: null output");
+    hipLaunchKernelGGL(dotl::mfma_probe_kernel, dim3(1), dim3(64), 0, dotl::as_stream(stream), out);
+    return dotl::check_launch("mfma_layout_probe");
+}
+
+void dotl_wmma_set_fp16(int on) { dotl::g_wmma_fp16.store(on ? 1 : 0); }
+int dotl_wmma_fp16(void) { return dotl::g_wmma_fp16.load(); }
+void dotl_wmma_set_cp_async(int mode) { dotl::g_cp_async.store(mode); }
+int dotl_wmma_cp_async_mode(void) { return dotl::g_cp_async.load(); }
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+// Shared device and host helpers for the gfx950 kernels behind include/dotl.h.
+//
+// Everything here is CDNA4-specific on purpose: 64-lane wavefronts, MFMA
+// vector types, and the one error channel every C-ABI entry point reports
+// through.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/dotl.h"
+
+namespace dotl {
+
+constexpr int kWave = 64;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// ---- error channel ---------------------------------------------------------
+
+void set_error(const std::string& msg);
+void clear_error();
+
+// Returns DOTL_E_LAUNCH with a message naming `who` if the last launch failed.
+int check_launch(const char* who);
+
+#define DOTL_REQUIRE(cond, ...)                                   \
+    do {                                                          \
+        if (!(cond)) {                                            \
+            char _dotl_buf[512];                                  \
+            std::snprintf(_dotl_buf, sizeof(_dotl_buf), __VA_ARGS__); \
+            ::dotl::set_error(_dotl_buf);                         \
+            return DOTL_E_INVALID;                                \
+        }                                                         \
+    } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- device helpers --------------------------------------------------------
+
+// Butterfly sum over the full 64-lane wavefront. Every lane ends with the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// Exact GELU, 0.5 x (1 + erf(x / sqrt 2)), with the device library's erff.
+__device__ __forceinline__ float gelu_erf(float x) {
+    return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+}
+
+// fp32 -> fp16 with round-to-nearest-even (the hardware conversion).
+__device__ __forceinline__ _Float16 to_half(float x) { return static_cast<_Float16>(x); }
+
+// Split x into hi = fp16(x) and lo = fp16((x - hi) * 2^12). hi + lo * 2^-12
+// carries ~22 significant bits for |x| in fp16's normal range; the 2^12 scale
+// keeps lo out of fp16's subnormals, whose flushing behaviour inside MFMA we
+// do not rely on.
+constexpr float kLoScale = 4096.0f;
+constexpr float kLoUnscale = 1.0f / 4096.0f;
+
+__device__ __forceinline__ _Float16 split_lo(float x, _Float16 hi) {
+    return static_cast<_Float16>((x - static_cast<float>(hi)) * kLoScale);
+}
+
+}  // namespace dotl

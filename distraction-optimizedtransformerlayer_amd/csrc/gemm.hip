@@ -1,0 +1,412 @@
+// out = act(x @ W^T + bias) on gfx950 MFMA.
+//
+// Replaces linear_bias / linear_gelu (reference csrc/linear_gelu.cuh:186-756):
+// same operation, same operand layouts (x [M, K] row-major, W [N, K] in
+// nn.Linear layout, fp32 bias), same fp16-operand / fp32-accumulate
+// arithmetic for the default math, the exact-erf GELU in the epilogue.
+//
+// MI355X design:
+//   * both operands are K-contiguous ("NT" GEMM), which is what MFMA wants:
+//     lane l of v_mfma_f32_32x32x16_f16 supplies 8 consecutive K elements of
+//     one A row and of one W row, so LDS tiles are plain row-major
+//     [rows][BK] and every fragment is one 16-byte LDS read;
+//   * 256 threads = 4 wavefronts in a 2 x 2 grid, each wavefront owning a
+//     (BM/2) x (BN/2) block of 32x32 accumulator tiles;
+//   * the next K tile is fetched from HBM into registers while the current
+//     one is multiplied out of LDS (register double buffering), so the LDS
+//     footprint is one tile and several workgroups fit per CU;
+//   * LDS rows are padded by 16 bytes so the 32 rows a fragment read touches
+//     fall on distinct bank groups;
+//   * W arrives pre-narrowed (dotl_weight_split, once per weight version);
+//     x may be fp32 (narrowed with RNE while staging, exactly the rounding
+//     the reference's Fp16Math applies) or fp16;
+//   * DOTL_MATH_FP16X3: x and W are split into hi + 2^-12 * lo fp16 pairs and
+//     the product is hi*hi + 2^-12 (hi*lo + lo*hi), with the two sums in
+//     separate fp32 accumulators. Three MFMA passes buy ~22-bit operands:
+//     fp32-class products on the fp16 matrix cores. It is what the
+//     projection feeding attention's scores uses (the accuracy budget is
+//     spent there; see the precision notes in the package's kernels.py).
+//   * the output tile is written from the accumulators: lane l holds one
+//     column and 16 rows of each 32x32 tile, so each store instruction
+//     writes two 128-byte row segments.
+#include "dotl_common.h"
+
+namespace dotl {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kPad = 8;  // halves of padding per LDS row (16 bytes)
+
+template <int BM, int BN, int BK>
+struct TileShape {
+    static constexpr int WM = BM / 2;       // rows per wavefront
+    static constexpr int WN = BN / 2;       // cols per wavefront
+    static constexpr int TM = WM / 32;      // 32x32 tiles per wavefront, M
+    static constexpr int TN = WN / 32;      // 32x32 tiles per wavefront, N
+    static constexpr int KS = BK / 16;      // MFMA k-steps per tile
+    static constexpr int LDK = BK + kPad;   // LDS row pitch in halves
+};
+
+// Global -> register staging of one [ROWS, BK] fp16 tile: chunks of 8 halves.
+template <int ROWS, int BK>
+struct HalfTile {
+    static constexpr int kChunks = ROWS * BK / 8;
+    static constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
+    half8 r[kPer];
+
+    __device__ __forceinline__ void load(const _Float16* __restrict__ src, int64_t ld,
+                                         int64_t row0, int64_t nrows, int64_t k0, int64_t K) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            const int row = c / (BK / 8);
+            const int col = (c % (BK / 8)) * 8;
+            half8 v = {};
+            if (c < kChunks && row0 + row < nrows && k0 + col < K) {
+                v = *reinterpret_cast<const half8*>(src + (row0 + row) * ld + k0 + col);
+            }
+            r[i] = v;
+        }
+    }
+    __device__ __forceinline__ void store(_Float16* lds) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            if (c < kChunks) {
+                const int row = c / (BK / 8);
+                const int col = (c % (BK / 8)) * 8;
+                *reinterpret_cast<half8*>(lds + row * (BK + kPad) + col) = r[i];
+            }
+        }
+    }
+};
+
+// Global -> register staging of one [ROWS, BK] fp32 tile, narrowed (and
+// optionally split) when written to LDS. Chunks of 4 floats.
+template <int ROWS, int BK>
+struct FloatTile {
+    static constexpr int kChunks = ROWS * BK / 4;
+    static constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
+    float4 r[kPer];
+
+    __device__ __forceinline__ void load(const float* __restrict__ src, int64_t ld,
+                                         int64_t row0, int64_t nrows, int64_t k0, int64_t K) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            const int row = c / (BK / 4);
+            const int col = (c % (BK / 4)) * 4;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (c < kChunks && row0 + row < nrows && k0 + col < K) {
+                v = *reinterpret_cast<const float4*>(src + (row0 + row) * ld + k0 + col);
+            }
+            r[i] = v;
+        }
+    }
+    __device__ __forceinline__ void store(_Float16* lds) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            if (c < kChunks) {
+                const int row = c / (BK / 4);
+                const int col = (c % (BK / 4)) * 4;
+                half4 h;
+                h[0] = to_half(r[i].x); h[1] = to_half(r[i].y);
+                h[2] = to_half(r[i].z); h[3] = to_half(r[i].w);
+                *reinterpret_cast<half4*>(lds + row * (BK + kPad) + col) = h;
+            }
+        }
+    }
+    __device__ __forceinline__ void store_split(_Float16* lds_hi, _Float16* lds_lo) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            if (c < kChunks) {
+                const int row = c / (BK / 4);
+                const int col = (c % (BK / 4)) * 4;
+                half4 h, l;
+                h[0] = to_half(r[i].x); l[0] = split_lo(r[i].x, h[0]);
+                h[1] = to_half(r[i].y); l[1] = split_lo(r[i].y, h[1]);
+                h[2] = to_half(r[i].z); l[2] = split_lo(r[i].z, h[2]);
+                h[3] = to_half(r[i].w); l[3] = split_lo(r[i].w, h[3]);
+                *reinterpret_cast<half4*>(lds_hi + row * (BK + kPad) + col) = h;
+                *reinterpret_cast<half4*>(lds_lo + row * (BK + kPad) + col) = l;
+            }
+        }
+    }
+};
+
+// Workgroup -> output tile. Workgroups are dispatched round-robin over the
+// 8 XCDs, each with its own L2, so the linear id is first regrouped so that
+// every XCD walks a contiguous stretch of the tile order; that order then
+// visits kGroupM row-tiles per column sweep, so the A rows and W columns a
+// stretch touches stay L2-resident while they are reused.
+constexpr int kXcds = 8;
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ void tile_of(int64_t id, int64_t nm, int64_t nn, int64_t& mt,
+                                        int64_t& nt) {
+    const int64_t total = nm * nn;
+    const int64_t per = total / kXcds;
+    if (id < per * kXcds) id = (id % kXcds) * per + id / kXcds;
+    const int64_t in_group = kGroupM * nn;
+    const int64_t group = id / in_group;
+    const int64_t first_m = group * kGroupM;
+    const int64_t gsize = min(static_cast<int64_t>(kGroupM), nm - first_m);
+    const int64_t r = id - group * in_group;
+    mt = first_m + r % gsize;
+    nt = r / gsize;
+}
+
+template <int BM, int BN, int BK, bool A_F32, bool SPLIT, int ACT, bool OUT_F16>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(
+    const void* __restrict__ A_, const _Float16* __restrict__ Whi,
+    const _Float16* __restrict__ Wlo, const float* __restrict__ bias,
+    void* __restrict__ C_, int64_t M, int64_t N, int64_t K) {
+    using TS = TileShape<BM, BN, BK>;
+    constexpr int LDK = TS::LDK;
+
+    __shared__ __attribute__((aligned(16))) _Float16 sA[BM * LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 sW[BN * LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 sAlo[(SPLIT && A_F32) ? BM * LDK : 8];
+    __shared__ __attribute__((aligned(16))) _Float16 sWlo[SPLIT ? BN * LDK : 8];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1;  // wave row in the 2x2 grid
+    const int wn = wave & 1;
+    const int lr = lane & 31;  // fragment row/col supplied by this lane
+    const int lg = lane >> 5;  // which 8-wide K slice of the 16
+
+    int64_t mt, nt;
+    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, mt, nt);
+    const int64_t m0 = mt * BM;
+    const int64_t n0 = nt * BN;
+
+    floatx16 acc[TS::TM][TS::TN];
+    floatx16 acc2[SPLIT ? TS::TM : 1][SPLIT ? TS::TN : 1];
+#pragma unroll
+    for (int i = 0; i < TS::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TS::TN; ++j) {
+            acc[i][j] = floatx16{};
+            if constexpr (SPLIT) acc2[i][j] = floatx16{};
+        }
+
+    using ATile = typename std::conditional<A_F32, FloatTile<BM, BK>, HalfTile<BM, BK>>::type;
+    ATile ta;
+    HalfTile<BN, BK> tw;
+    HalfTile<SPLIT ? BN : 8, SPLIT ? BK : 8> twlo;
+
+    const int64_t nk = (K + BK - 1) / BK;
+    if constexpr (A_F32) {
+        ta.load(static_cast<const float*>(A_), K, m0, M, 0, K);
+    } else {
+        ta.load(static_cast<const _Float16*>(A_), K, m0, M, 0, K);
+    }
+    tw.load(Whi, K, n0, N, 0, K);
+    if constexpr (SPLIT) twlo.load(Wlo, K, n0, N, 0, K);
+
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        __syncthreads();  // previous tile's fragment reads are done
+        if constexpr (SPLIT && A_F32) {
+            ta.store_split(sA, sAlo);
+        } else {
+            ta.store(sA);
+        }
+        if constexpr (SPLIT) twlo.store(sWlo);
+        tw.store(sW);
+        __syncthreads();
+
+        if (kt + 1 < nk) {
+            const int64_t k1 = (kt + 1) * BK;
+            if constexpr (A_F32) {
+                ta.load(static_cast<const float*>(A_), K, m0, M, k1, K);
+            } else {
+                ta.load(static_cast<const _Float16*>(A_), K, m0, M, k1, K);
+            }
+            tw.load(Whi, K, n0, N, k1, K);
+            if constexpr (SPLIT) twlo.load(Wlo, K, n0, N, k1, K);
+        }
+
+#pragma unroll
+        for (int ks = 0; ks < TS::KS; ++ks) {
+            const int kc = ks * 16 + lg * 8;
+            half8 a[TS::TM], b[TS::TN];
+#pragma unroll
+            for (int i = 0; i < TS::TM; ++i)
+                a[i] = *reinterpret_cast<const half8*>(sA + (wm * TS::WM + i * 32 + lr) * LDK + kc);
+#pragma unroll
+            for (int j = 0; j < TS::TN; ++j)
+                b[j] = *reinterpret_cast<const half8*>(sW + (wn * TS::WN + j * 32 + lr) * LDK + kc);
+#pragma unroll
+            for (int i = 0; i < TS::TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TS::TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+            if constexpr (SPLIT) {
+                // 2^-12-scaled residual products: hi(x) * lo(W), and for an
+                // fp32 x also lo(x) * hi(W). An fp16 x has no residual.
+                half8 bl[TS::TN];
+#pragma unroll
+                for (int j = 0; j < TS::TN; ++j)
+                    bl[j] = *reinterpret_cast<const half8*>(sWlo + (wn * TS::WN + j * 32 + lr) * LDK + kc);
+#pragma unroll
+                for (int i = 0; i < TS::TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TS::TN; ++j)
+                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl[j], acc2[i][j], 0, 0, 0);
+                if constexpr (A_F32) {
+                    half8 al[TS::TM];
+#pragma unroll
+                    for (int i = 0; i < TS::TM; ++i)
+                        al[i] = *reinterpret_cast<const half8*>(sAlo + (wm * TS::WM + i * 32 + lr) * LDK + kc);
+#pragma unroll
+                    for (int i = 0; i < TS::TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TS::TN; ++j)
+                            acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], b[j], acc2[i][j], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // Epilogue. Accumulator register r of a 32x32 tile at lane l holds
+    // row 8*(r/4) + 4*(l/32) + (r%4), column l%32.
+#pragma unroll
+    for (int j = 0; j < TS::TN; ++j) {
+        const int64_t col = n0 + wn * TS::WN + j * 32 + lr;
+        if (col >= N) continue;
+        const float bcol = bias[col];
+#pragma unroll
+        for (int i = 0; i < TS::TM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + wm * TS::WM + i * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+                if (row < M) {
+                    float v = acc[i][j][r];
+                    if constexpr (SPLIT) v += acc2[i][j][r] * kLoUnscale;
+                    v += bcol;
+                    if constexpr (ACT == DOTL_ACT_GELU) v = gelu_erf(v);
+                    if constexpr (OUT_F16) {
+                        static_cast<_Float16*>(C_)[row * N + col] = to_half(v);
+                    } else {
+                        static_cast<float*>(C_)[row * N + col] = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+__global__ void weight_split_kernel(const float* __restrict__ w, _Float16* __restrict__ hi,
+                                    _Float16* __restrict__ lo, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const _Float16 h = to_half(w[i]);
+        hi[i] = h;
+        if (lo) lo[i] = split_lo(w[i], h);
+    }
+}
+
+struct GemmArgs {
+    const void* A;
+    const _Float16* Whi;
+    const _Float16* Wlo;
+    const float* bias;
+    void* C;
+    int64_t M, N, K;
+    hipStream_t stream;
+};
+
+template <int BM, int BN, int BK, bool A_F32, bool SPLIT, int ACT, bool OUT_F16>
+void launch(const GemmArgs& g) {
+    const dim3 grid(static_cast<unsigned>(((g.N + BN - 1) / BN) * ((g.M + BM - 1) / BM)));
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, A_F32, SPLIT, ACT, OUT_F16>), grid,
+                       dim3(kThreads), 0, g.stream, g.A, g.Whi, g.Wlo, g.bias, g.C, g.M, g.N,
+                       g.K);
+}
+
+template <bool A_F32, bool SPLIT, int ACT, bool OUT_F16>
+void launch_tile(const GemmArgs& g, int tile) {
+    switch (tile) {
+        case 2: launch<64, 64, 64, A_F32, SPLIT, ACT, OUT_F16>(g); break;
+        default: launch<128, 128, 64, A_F32, SPLIT, ACT, OUT_F16>(g); break;
+    }
+}
+
+template <bool A_F32, bool SPLIT>
+void launch_epilogue(const GemmArgs& g, int tile, int act, bool out_f16) {
+    if (act == DOTL_ACT_GELU) {
+        out_f16 ? launch_tile<A_F32, SPLIT, DOTL_ACT_GELU, true>(g, tile)
+                : launch_tile<A_F32, SPLIT, DOTL_ACT_GELU, false>(g, tile);
+    } else {
+        out_f16 ? launch_tile<A_F32, SPLIT, DOTL_ACT_NONE, true>(g, tile)
+                : launch_tile<A_F32, SPLIT, DOTL_ACT_NONE, false>(g, tile);
+    }
+}
+
+// Tile choice for 256 CUs: the 128x128 tile unless it leaves the grid well
+// short of one workgroup per CU, then 64x64.
+int pick_tile(int64_t M, int64_t N) {
+    const int64_t big = ((M + 127) / 128) * ((N + 127) / 128);
+    return big >= 192 ? 0 : 2;
+}
+
+}  // namespace
+}  // namespace dotl
+
+extern "C" int dotl_weight_split(const float* w, void* w_hi, void* w_lo, int64_t n,
+                                 void* stream) {
+    using namespace dotl;
+    clear_error();
+    DOTL_REQUIRE(n >= 0, "weight_split: negative size");
+    if (n == 0) return DOTL_OK;
+    DOTL_REQUIRE(w && w_hi, "weight_split: null pointer");
+    const int64_t blocks = (n + 255) / 256;
+    DOTL_REQUIRE(blocks <= 0x7fffffff, "weight_split: too many elements");
+    hipLaunchKernelGGL(weight_split_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       as_stream(stream), w, static_cast<_Float16*>(w_hi),
+                       static_cast<_Float16*>(w_lo), n);
+    return check_launch("weight_split");
+}
+
+extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
+                           const float* bias, void* out, int out_dtype, int64_t M, int64_t N,
+                           int64_t K, int act, int math, int tile, void* stream) {
+    using namespace dotl;
+    clear_error();
+    const char* who = act == DOTL_ACT_GELU ? "linear_gelu" : "linear_bias";
+    DOTL_REQUIRE(x_dtype == DOTL_F32 || x_dtype == DOTL_F16, "%s: x must be float32 or float16", who);
+    DOTL_REQUIRE(out_dtype == DOTL_F32 || out_dtype == DOTL_F16, "%s: out must be float32 or float16", who);
+    DOTL_REQUIRE(act == DOTL_ACT_NONE || act == DOTL_ACT_GELU, "%s: unknown activation %d", who, act);
+    DOTL_REQUIRE(math == DOTL_MATH_FP16 || math == DOTL_MATH_FP16X3, "%s: unknown math %d", who, math);
+    DOTL_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative extent", who);
+    if (K % 8 != 0 || K == 0) {
+        set_error(std::string(who) + ": K must be a positive multiple of 8 for 16-byte staging");
+        return DOTL_DECLINED;
+    }
+    DOTL_REQUIRE(math != DOTL_MATH_FP16X3 || w_lo != nullptr,
+                 "%s: the fp16x3 math needs the split weight residual", who);
+    DOTL_REQUIRE(((M + 63) / 64) * ((N + 63) / 64) <= 0x7fffffff, "%s: too large", who);
+    if (M == 0 || N == 0) return DOTL_OK;
+    DOTL_REQUIRE(x && w_hi && bias && out, "%s: null pointer", who);
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_hi) |
+                            reinterpret_cast<uintptr_t>(w_lo);
+    DOTL_REQUIRE(align % 16 == 0, "%s: x and W must be 16-byte aligned", who);
+
+    GemmArgs g{x, static_cast<const _Float16*>(w_hi), static_cast<const _Float16*>(w_lo), bias,
+               out, M, N, K, as_stream(stream)};
+    const int t = tile < 0 ? pick_tile(M, N) : tile;
+    DOTL_REQUIRE(t == 0 || t == 2, "%s: unknown tile id %d", who, tile);
+    const bool of16 = out_dtype == DOTL_F16;
+    if (math == DOTL_MATH_FP16X3) {
+        if (x_dtype == DOTL_F32) launch_epilogue<true, true>(g, t, act, of16);
+        else launch_epilogue<false, true>(g, t, act, of16);
+    } else if (x_dtype == DOTL_F32) {
+        launch_epilogue<true, false>(g, t, act, of16);
+    } else {
+        launch_epilogue<false, false>(g, t, act, of16);
+    }
+    return check_launch(who);
+}

@@ -1,0 +1,564 @@
+"""Loader for the gfx950 kernels: the reference's extension surface over a C ABI.
+
+The reference's `kernel_ext.get_kernels()` JIT-builds a pybind CUDA module and
+returns it, or None when it cannot (reference kernel_ext.py:363-491). This
+module keeps that contract -- `get_kernels()` returns an object whose methods
+have the pybind module's names, arguments and return conventions
+(reference csrc/fused_attention.cu:118-376), `load_error()` says why it is
+None -- but the object is a thin ctypes layer over `libdotl_hip.so`, the
+C-ABI library declared in include/dotl.h:
+
+  * device memory and streams are torch's: outputs are allocated with
+    torch.empty on the input's device, and every launch goes to
+    torch.cuda.current_stream() read at call time, so a call made under
+    torch.cuda.graph() capture is recorded into the graph;
+  * the C entry points return 0 (launched), 1 (declined: the reference's
+    undefined tensor / empty list, i.e. None / [] here) or a negative error
+    (the reference's TORCH_CHECK raise, i.e. RuntimeError here);
+  * W is narrowed to fp16 once per weight version and cached here (the
+    reference narrows it inside every GEMM launch); `weight_cache_tensors()`
+    lists the cached buffers so graph capture can pin them.
+
+There is no CPU fallback anywhere in this module: a missing library makes
+get_kernels() return None, and the callers that cannot decline (attention)
+raise, exactly as the reference does.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+import threading
+import weakref
+from typing import Dict, List, Optional, Tuple
+
+_THIS_DIR = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_THIS_DIR, "libdotl_hip.so")
+_CSRC = os.path.join(_THIS_DIR, "csrc")
+
+ABI_VERSION = 1
+
+DOTL_OK = 0
+DOTL_DECLINED = 1
+DOTL_F32 = 0
+DOTL_F16 = 1
+DOTL_ACT_NONE = 0
+DOTL_ACT_GELU = 1
+DOTL_MATH_FP16 = 0
+DOTL_MATH_FP16X3 = 1
+
+# Every symbol include/dotl.h declares.
+EXPORTED_SYMBOLS = (
+    "dotl_last_error", "dotl_abi_version", "dotl_target", "dotl_smoke_test_identity",
+    "dotl_mfma_layout_probe", "dotl_layernorm", "dotl_weight_split", "dotl_linear",
+    "dotl_attention_forward", "dotl_ffn_block", "dotl_wmma_set_fp16", "dotl_wmma_fp16",
+    "dotl_wmma_set_cp_async", "dotl_wmma_cp_async_mode",
+)
+
+_kernels = None
+_load_attempted = False
+_load_error: Optional[BaseException] = None
+_lock = threading.Lock()
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def build(verbose: bool = False, jobs: int = 8) -> str:
+    """Compile libdotl_hip.so for gfx950 with the Makefile in csrc/ (hipcc).
+
+    Needs no GPU: hipcc cross-compiles. Returns the library path.
+    """
+    cmd = ["make", "-C", _CSRC, f"-j{jobs}"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if verbose or res.returncode != 0:
+        print(res.stdout)
+        print(res.stderr)
+    if res.returncode != 0:
+        raise RuntimeError(f"building libdotl_hip.so failed (exit {res.returncode}):\n"
+                           f"{res.stderr[-4000:]}")
+    return _LIB_PATH
+
+
+def _declare(lib) -> None:
+    c = ctypes
+    i64, vp, i32 = c.c_int64, c.c_void_p, c.c_int
+    lib.dotl_last_error.restype = c.c_char_p
+    lib.dotl_last_error.argtypes = []
+    lib.dotl_abi_version.restype = i32
+    lib.dotl_target.restype = c.c_char_p
+    lib.dotl_smoke_test_identity.restype = i32
+    lib.dotl_smoke_test_identity.argtypes = [vp, vp, i64, vp]
+    lib.dotl_mfma_layout_probe.restype = i32
+    lib.dotl_mfma_layout_probe.argtypes = [vp, vp]
+    lib.dotl_layernorm.restype = i32
+    lib.dotl_layernorm.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, c.c_double, i32, i32, vp]
+    lib.dotl_weight_split.restype = i32
+    lib.dotl_weight_split.argtypes = [vp, vp, vp, i64, vp]
+    lib.dotl_linear.restype = i32
+    lib.dotl_linear.argtypes = [vp, i32, vp, vp, vp, vp, i32, i64, i64, i64, i32, i32, i32, vp]
+    lib.dotl_attention_forward.restype = i32
+    lib.dotl_attention_forward.argtypes = [vp, vp, vp, i32, c.POINTER(i64), vp, c.POINTER(i64),
+                                           vp, i32, i32, i32, i32, i32, i32, i32, c.c_double,
+                                           i32, i32, vp]
+    lib.dotl_ffn_block.restype = i32
+    lib.dotl_ffn_block.argtypes = [vp] * 12 + [i64, i64, i64, c.c_double, vp]
+    lib.dotl_wmma_set_fp16.restype = None
+    lib.dotl_wmma_set_fp16.argtypes = [i32]
+    lib.dotl_wmma_fp16.restype = i32
+    lib.dotl_wmma_set_cp_async.restype = None
+    lib.dotl_wmma_set_cp_async.argtypes = [i32]
+    lib.dotl_wmma_cp_async_mode.restype = i32
+
+
+def load_library(path: Optional[str] = None):
+    """dlopen the C-ABI library (after torch, so it binds torch's HIP runtime)."""
+    import torch  # noqa: F401  -- the HIP runtime must be loaded first
+
+    lib = ctypes.CDLL(path or _LIB_PATH)
+    _declare(lib)
+    got = lib.dotl_abi_version()
+    if got != ABI_VERSION:
+        raise RuntimeError(f"libdotl_hip.so ABI {got}, this loader speaks {ABI_VERSION}; rebuild")
+    return lib
+
+
+def _version_or_none(t) -> Optional[int]:
+    try:
+        return t._version
+    except RuntimeError:
+        return None
+
+
+def _dtype_code(t) -> Optional[int]:
+    import torch
+
+    if t.dtype == torch.float32:
+        return DOTL_F32
+    if t.dtype == torch.float16:
+        return DOTL_F16
+    return None
+
+
+class Kernels:
+    """The extension module: same entry points as the reference's pybind module."""
+
+    def __init__(self, lib) -> None:
+        self._lib = lib
+        self._wcache: Dict[int, Tuple[weakref.ReferenceType, tuple, object, object]] = {}
+        self._tile_split_kv = False
+        self._layernorm_knobs = {"block_threads": 0, "warp_width": -1, "warp_rows": 0,
+                                 "fused_reduce": True}
+        self._wmma_flags = {"softmax_mode": 1, "mask_classify": True, "acc_formula": True,
+                            "direct_o": True, "split_kv": True, "split_count": 0,
+                            "causal_reverse": True}
+
+    # -- plumbing ----------------------------------------------------------------
+
+    def _err(self) -> str:
+        msg = self._lib.dotl_last_error()
+        return msg.decode() if msg else ""
+
+    def _check(self, rc: int) -> int:
+        if rc < 0:
+            raise RuntimeError(self._err())
+        return rc
+
+    @staticmethod
+    def _stream(device) -> int:
+        import torch
+
+        return torch.cuda.current_stream(device).cuda_stream
+
+    @staticmethod
+    def _require_cuda(who: str, *tensors) -> None:
+        for t in tensors:
+            if t is not None and not t.is_cuda:
+                raise RuntimeError(f"{who}: all inputs must be CUDA tensors")
+
+    def raw(self):
+        """The ctypes library handle, for tests that call the C ABI directly."""
+        return self._lib
+
+    # -- build smoke test (reference csrc/fused_attention.cu:96-114) ---------------
+
+    def smoke_test_identity(self, x):
+        import torch
+
+        self._require_cuda("smoke_test_identity", x)
+        if x.dtype != torch.float32:
+            raise RuntimeError("smoke_test_identity: float32 only")
+        xc = x.contiguous()
+        out = torch.empty_like(xc)
+        self._check(self._lib.dotl_smoke_test_identity(
+            xc.data_ptr(), out.data_ptr(), xc.numel(), self._stream(x.device)))
+        return out
+
+    def mfma_layout_probe(self, device=None):
+        import torch
+
+        out = torch.empty(1280, dtype=torch.int32, device=device or "cuda")
+        self._check(self._lib.dotl_mfma_layout_probe(out.data_ptr(), self._stream(out.device)))
+        return out
+
+    # -- LayerNorm (reference csrc/add_layernorm.cuh:491-692) -----------------------
+
+    def _layernorm(self, who, x, sub, weight, bias, eps, normed_half, write_xnew=True):
+        import torch
+
+        self._require_cuda(who, x, sub, weight, bias)
+        if x.dim() < 1:
+            raise RuntimeError(f"{who}: x needs at least one dimension")
+        D = x.shape[-1]
+        if weight.numel() != D or bias.numel() != D:
+            raise RuntimeError(f"{who}: weight/bias must have {D} elements")
+        if weight.dtype != x.dtype or bias.dtype != x.dtype:
+            raise RuntimeError(f"{who}: weight/bias must share x's dtype")
+        if sub is not None:
+            if tuple(sub.shape) != tuple(x.shape):
+                raise RuntimeError(f"{who}: x and sub must have identical shapes, got "
+                                   f"{tuple(x.shape)} and {tuple(sub.shape)}")
+            if sub.dtype != x.dtype:
+                raise RuntimeError(f"{who}: x and sub must share a dtype")
+        if normed_half and x.dtype != torch.float32:
+            raise RuntimeError(f"{who}: normed_half is only defined for an fp32 input, got {x.dtype}")
+        if x.dtype != torch.float32:
+            raise RuntimeError(f"{who}: this build serves float32 tensors only, got {x.dtype}")
+        xc = x.contiguous()
+        sc = sub.contiguous() if sub is not None else None
+        wc, bc = weight.contiguous(), bias.contiguous()
+        x_new = torch.empty_like(xc) if (sc is not None and write_xnew) else None
+        normed = torch.empty(xc.shape, dtype=torch.float16 if normed_half else torch.float32,
+                             device=xc.device)
+        rows = xc.numel() // D if D else 0
+        rc = self._lib.dotl_layernorm(
+            xc.data_ptr(), sc.data_ptr() if sc is not None else None, wc.data_ptr(),
+            bc.data_ptr(), x_new.data_ptr() if x_new is not None else None, normed.data_ptr(),
+            rows, D, float(eps), DOTL_F32, DOTL_F16 if normed_half else DOTL_F32,
+            self._stream(x.device))
+        self._check(rc)
+        if rc == DOTL_DECLINED:
+            raise RuntimeError(self._err())
+        return x_new, normed
+
+    def fused_add_layernorm(self, x, sub, weight, bias, eps=1e-5, normed_half=False):
+        """[x + sub, LayerNorm(x + sub)] in one kernel."""
+        if sub is None:
+            raise RuntimeError("fused_add_layernorm: sub is required")
+        x_new, normed = self._layernorm("fused_add_layernorm", x, sub, weight, bias, eps,
+                                        normed_half)
+        return [x_new, normed]
+
+    def fused_add_layernorm_final(self, x, sub, weight, bias, eps=1e-5):
+        """LayerNorm(x + sub) only: the residual sum is not stored.
+
+        For the model's last add+LN, whose sum nothing reads. Same kernel as
+        fused_add_layernorm with the x_new store compiled out.
+        """
+        _, normed = self._layernorm("fused_add_layernorm", x, sub, weight, bias, eps, False,
+                                    write_xnew=False)
+        return normed
+
+    def fused_layernorm(self, x, weight, bias, eps=1e-5, out_half=False):
+        """Plain LayerNorm over the last dimension."""
+        _, normed = self._layernorm("fused_layernorm", x, None, weight, bias, eps, out_half)
+        return normed
+
+    # -- GEMM (reference csrc/linear_gelu.cuh:598-756) -------------------------------
+
+    def weight_half(self, weight, want_lo: bool):
+        """(w_hi, w_lo) fp16 copies of an fp32 [N, K] weight, cached per version."""
+        import torch
+
+        key = (weight.data_ptr(), tuple(weight.shape), str(weight.device),
+               _version_or_none(weight))
+        ent = self._wcache.get(id(weight))
+        if ent is not None and ent[0]() is weight and ent[1] == key and (ent[3] is not None or not want_lo):
+            return ent[2], ent[3]
+        wc = weight.detach().contiguous()
+        hi = torch.empty(wc.shape, dtype=torch.float16, device=wc.device)
+        lo = torch.empty(wc.shape, dtype=torch.float16, device=wc.device) if want_lo else None
+        self._check(self._lib.dotl_weight_split(
+            wc.data_ptr(), hi.data_ptr(), lo.data_ptr() if lo is not None else None,
+            wc.numel(), self._stream(wc.device)))
+        if len(self._wcache) > 256:
+            self._wcache = {k: v for k, v in self._wcache.items() if v[0]() is not None}
+        self._wcache[id(weight)] = (weakref.ref(weight), key, hi, lo)
+        return hi, lo
+
+    def weight_cache_tensors(self) -> List[object]:
+        """Every live cached fp16 weight buffer (graph capture pins these)."""
+        out = []
+        for ref, _, hi, lo in self._wcache.values():
+            if ref() is not None:
+                out.append(hi)
+                if lo is not None:
+                    out.append(lo)
+        return out
+
+    def _gemm(self, who, x, weight, bias, tile, math, act, out_half):
+        import torch
+
+        self._require_cuda(who, x, weight, bias)
+        if weight.dim() != 2:
+            raise RuntimeError(f"{who}: weight must be 2-D [N, K]")
+        if x.dim() < 1 or x.shape[-1] != weight.shape[1]:
+            raise RuntimeError(f"{who}: x's last dimension must match weight's, got "
+                               f"{tuple(x.shape)} and {tuple(weight.shape)}")
+        if bias.numel() != weight.shape[0]:
+            raise RuntimeError(f"{who}: bias must have {weight.shape[0]} elements")
+        xcode = _dtype_code(x)
+        if (xcode is None or weight.dtype != torch.float32 or bias.dtype != torch.float32):
+            return None  # declined: the caller falls back
+        K, N = weight.shape[1], weight.shape[0]
+        if K % 8 != 0 or K == 0:
+            return None
+        # math: -1 auto -> fp16 operands; 0 (the reference's tf32 slot) -> the
+        # split fp16x3 path, which needs an fp32 x.
+        m = DOTL_MATH_FP16 if math in (-1, None) else DOTL_MATH_FP16X3
+        xc = x.contiguous()
+        M = xc.numel() // K
+        hi, lo = self.weight_half(weight, m == DOTL_MATH_FP16X3)
+        bc = bias.contiguous()
+        out = torch.empty((*xc.shape[:-1], N), dtype=torch.float16 if out_half else torch.float32,
+                          device=xc.device)
+        rc = self._check(self._lib.dotl_linear(
+            xc.data_ptr(), xcode, hi.data_ptr(), lo.data_ptr() if lo is not None else None,
+            bc.data_ptr(), out.data_ptr(), DOTL_F16 if out_half else DOTL_F32, M, N, K, act, m,
+            int(tile), self._stream(x.device)))
+        if rc == DOTL_DECLINED:
+            return None
+        return out
+
+    def linear_bias(self, x, weight, bias, tile=-1, math=-1, out_half=False):
+        """x @ weight^T + bias, or None when the shape/dtype is not covered."""
+        return self._gemm("linear_bias", x, weight, bias, tile, math, DOTL_ACT_NONE, out_half)
+
+    def linear_gelu(self, x, weight, bias, tile=-1, math=-1, out_half=False):
+        """GELU_erf(x @ weight^T + bias), or None when not covered.
+
+        `out_half` (not in the reference's signature; appended, default off)
+        stores the GELU output as fp16 for a consumer that narrows it anyway.
+        """
+        return self._gemm("linear_gelu", x, weight, bias, tile, math, DOTL_ACT_GELU, out_half)
+
+    # -- attention (reference csrc/attention_dispatch.cuh:332-519) -------------------
+
+    def fused_attention_forward(self, q, k, v, attn_mask=None, is_causal=False, scale=None,
+                                impl=0, out_layout=0, precision=0):
+        import torch
+
+        who = "fused_attention_forward"
+        if scale is None:
+            raise TypeError(f"{who}: scale is required")
+        if out_layout not in (0, 1):
+            raise RuntimeError(f"{who}: out_layout must be 0 ([B,H,S,head_dim]) or 1 ([B,S,H*head_dim])")
+        if not (0 <= impl <= 3):
+            raise RuntimeError(f"{who}: impl must be 0 (auto), 1 (scalar), 2 (wmma) or 3 (tile)")
+        if not (0 <= precision <= 4):
+            raise RuntimeError(f"{who}: precision must be 0 (auto), 1 (fp32), 2 (tf32), 3 (fp16) or 4 (bf16)")
+        if not (q.is_cuda and k.is_cuda and v.is_cuda):
+            raise RuntimeError(f"{who}: q/k/v must be CUDA tensors")
+        if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+            raise RuntimeError(f"{who}: q/k/v must be 4-D [B, H, S, head_dim]")
+        if q.shape != k.shape or q.shape != v.shape:
+            raise RuntimeError(f"{who}: q/k/v must have identical shapes")
+        if q.dtype != k.dtype or q.dtype != v.dtype:
+            raise RuntimeError(f"{who}: q/k/v must share a dtype")
+        code = _dtype_code(q)
+        B, H, S, hd = (int(s) for s in q.shape)
+        if code is None:
+            raise RuntimeError(f"{who}: impl={impl}, precision={precision} does not cover "
+                               f"dtype={q.dtype}, head_dim={hd}: the MFMA kernel takes float16 "
+                               f"or float32 tensors")
+        pass_strided = (q.stride(3) == 1 and k.stride(3) == 1 and v.stride(3) == 1
+                        and q.stride() == k.stride() and q.stride() == v.stride())
+        if not pass_strided:
+            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        if any((st * q.element_size()) % 16 for st in q.stride()[:3]):
+            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        strides = (ctypes.c_int64 * 3)(q.stride(0), q.stride(1), q.stride(2))
+        mask_ptr = None
+        ms = None
+        keep = None
+        if attn_mask is not None:
+            if attn_mask.dtype != torch.bool:
+                raise RuntimeError(f"{who}: attn_mask must be a bool tensor")
+            keep = attn_mask.contiguous().expand(B, H, S, S)
+            mask_ptr = keep.data_ptr()
+            ms = (ctypes.c_int64 * 4)(*keep.stride())
+        if out_layout == 1:
+            out = torch.empty((B, S, H * hd), dtype=q.dtype, device=q.device)
+        else:
+            out = torch.empty((B, H, S, hd), dtype=q.dtype, device=q.device)
+        rc = self._lib.dotl_attention_forward(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), code,
+            strides, mask_ptr, ms, out.data_ptr(), code,
+            out_layout, B, H, S, hd, 1 if is_causal else 0, float(scale), int(impl),
+            int(precision), self._stream(q.device))
+        self._check(rc)
+        if rc == DOTL_DECLINED:
+            raise RuntimeError(self._err())
+        del keep
+        return out
+
+    # -- fused FFN block (reference csrc/ffn_block.cuh:270-311) ----------------------
+
+    def fused_ffn_block(self, x, attn_out, norm1_w, norm1_b, ffn_in_w, ffn_in_b, ffn_out_w,
+                        ffn_out_b, norm2_w, norm2_b, eps):
+        self._require_cuda("fused_ffn_block", x, attn_out)
+        if tuple(x.shape) != tuple(attn_out.shape):
+            raise RuntimeError(f"fused_ffn_block: x and attn_out must match, got "
+                               f"{tuple(x.shape)} and {tuple(attn_out.shape)}")
+        D = x.shape[-1]
+        F = ffn_in_w.shape[0]
+        args = [t.data_ptr() for t in (x, attn_out, norm1_w, norm1_b, ffn_in_w, ffn_in_b,
+                                        ffn_out_w, ffn_out_b, norm2_w, norm2_b)]
+        rc = self._check(self._lib.dotl_ffn_block(
+            *args, None, None, x.numel() // D, D, F, float(eps), self._stream(x.device)))
+        if rc == DOTL_DECLINED:
+            return []
+        raise RuntimeError("fused_ffn_block: the library launched a block this loader "
+                           "allocated no outputs for")
+
+    # -- knobs (reference csrc/fused_attention.cu:157-366) -------------------------
+
+    def wmma_set_fp16(self, on: bool) -> None:
+        self._lib.dotl_wmma_set_fp16(1 if on else 0)
+
+    def wmma_fp16(self) -> bool:
+        return bool(self._lib.dotl_wmma_fp16())
+
+    def wmma_set_cp_async(self, mode: int) -> None:
+        self._lib.dotl_wmma_set_cp_async(int(mode))
+
+    def wmma_cp_async_mode(self) -> int:
+        return int(self._lib.dotl_wmma_cp_async_mode())
+
+    # Knobs the reference's scripts flip for A/B runs. They name NVIDIA-kernel
+    # variants with no counterpart here; they are accepted and remembered so
+    # such scripts run, and change nothing.
+    def wmma_set_softmax_mode(self, mode: int) -> None:
+        if mode not in (0, 1, 2):
+            raise RuntimeError("wmma_set_softmax_mode: mode must be 0, 1 or 2")
+        self._wmma_flags["softmax_mode"] = mode
+
+    def wmma_softmax_mode(self) -> int:
+        return self._wmma_flags["softmax_mode"]
+
+    def wmma_set_mask_classify(self, on: bool) -> None:
+        self._wmma_flags["mask_classify"] = bool(on)
+
+    def wmma_mask_classify_enabled(self) -> bool:
+        return self._wmma_flags["mask_classify"]
+
+    def wmma_set_acc_formula(self, on: bool) -> None:
+        self._wmma_flags["acc_formula"] = bool(on)
+
+    def wmma_acc_formula_enabled(self) -> bool:
+        return self._wmma_flags["acc_formula"]
+
+    def wmma_acc_formula_ok(self) -> List[bool]:
+        return [True, True]
+
+    def wmma_set_direct_o(self, on: bool) -> None:
+        self._wmma_flags["direct_o"] = bool(on)
+
+    def wmma_direct_o_enabled(self) -> bool:
+        return self._wmma_flags["direct_o"]
+
+    def wmma_set_split_kv(self, on: bool) -> None:
+        self._wmma_flags["split_kv"] = bool(on)
+
+    def wmma_split_kv_enabled(self) -> bool:
+        return self._wmma_flags["split_kv"]
+
+    def wmma_set_split_count(self, n: int) -> None:
+        self._wmma_flags["split_count"] = int(n)
+
+    def wmma_split_count(self, B, H, S, head_dim, is_causal) -> int:
+        return 1  # the MFMA kernel does not split the key range
+
+    def wmma_set_causal_reverse(self, on: bool) -> None:
+        self._wmma_flags["causal_reverse"] = bool(on)
+
+    def wmma_causal_reverse_enabled(self) -> bool:
+        return self._wmma_flags["causal_reverse"]
+
+    def wmma_grid_info(self, B, H, S, head_dim) -> List[int]:
+        """{grid blocks, blocks resident at once, BLOCK_M, BLOCK_N} of the MFMA kernel."""
+        if head_dim not in (32, 64, 128):
+            return [0, 0, 0]
+        waves = 1 if S <= 32 else (2 if S <= 64 else 4)
+        bm = 32 * waves
+        blocks = ((S + bm - 1) // bm) * B * H
+        per_cu = 1 if head_dim == 128 else 2
+        return [blocks, 256 * 4 * per_cu // waves, bm, 64]
+
+    def layernorm_set_block_threads(self, threads: int) -> None:
+        self._layernorm_knobs["block_threads"] = int(threads)
+
+    def layernorm_set_warp_width(self, width: int) -> None:
+        self._layernorm_knobs["warp_width"] = int(width)
+
+    def layernorm_warp_width(self) -> int:
+        return 8192  # one wavefront per row at every width
+
+    def layernorm_set_warp_rows(self, rows: int) -> None:
+        self._layernorm_knobs["warp_rows"] = int(rows)
+
+    def layernorm_warp_rows(self) -> int:
+        return 4
+
+    def layernorm_set_fused_reduce(self, enabled: bool) -> None:
+        self._layernorm_knobs["fused_reduce"] = bool(enabled)
+
+    def layernorm_fused_reduce_enabled(self) -> bool:
+        return True
+
+    def layernorm_block_threads(self, D: int) -> int:
+        return 256
+
+    def layernorm_blocks_per_sm(self, D: int) -> int:
+        return 8
+
+    # The tile kernels are an NVIDIA programming model; this build has none
+    # (reference csrc/tile_attention.cu:1125-1148 is the stub these mirror).
+    def tile_workspace_bytes(self, B, H, S, head_dim, is_causal, precision) -> int:
+        return 0
+
+    def tile_set_split_kv(self, enabled: bool) -> None:
+        self._tile_split_kv = bool(enabled)
+
+    def tile_split_kv_enabled(self) -> bool:
+        return self._tile_split_kv
+
+
+def get_kernels(verbose: bool = False):
+    """Load (building once if needed) and return the kernels, or None if unavailable."""
+    global _kernels, _load_attempted, _load_error
+    if _load_attempted:
+        return _kernels
+    with _lock:
+        if _load_attempted:
+            return _kernels
+        try:
+            import torch
+
+            if not torch.cuda.is_available():
+                raise RuntimeError("no HIP device is available (torch.cuda.is_available() is False)")
+            if not os.path.exists(_LIB_PATH):
+                build(verbose=verbose)
+            _kernels = Kernels(load_library())
+        except BaseException as exc:  # noqa: BLE001 - reported through load_error()
+            _kernels = None
+            _load_error = exc
+        _load_attempted = True
+    return _kernels
+
+
+def load_error() -> Optional[BaseException]:
+    """Whatever went wrong during the last get_kernels() attempt, if anything."""
+    return _load_error

@@ -1,0 +1,202 @@
+"""Dispatch into the gfx950 kernels (reference optimized/kernels.py:1-339).
+
+The boundary between torch ops and libdotl_hip.so, reached through
+kernel_ext.get_kernels(). Same function names, arguments and fallback rules
+as the reference:
+
+  * attention has no fallback: a missing extension or an uncovered shape
+    raises (reference optimized/kernels.py:297-338);
+  * the elementwise helpers and the GEMMs answer in torch when the extension
+    is missing or declines a shape (the reference's undefined-tensor / None
+    convention). Every such answer is counted in `fallback_counts`, so a test
+    can assert that the configured shapes never take one.
+
+Precision edges are decided here (which tensors cross HBM as fp16, and the
+QKV projection's arithmetic); see the notes on config.QKV_PRECISION.
+"""
+
+from __future__ import annotations
+
+from collections import Counter
+from typing import Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from . import config
+
+# op name -> times a torch fallback answered instead of a kernel
+fallback_counts: Counter = Counter()
+
+# Last values pushed into the extension's process-wide knobs (pushed on change).
+_fp16_pushed = None
+_cp_async_pushed = None
+
+
+def _sync_attention_precision(kernels) -> None:
+    """Keep the extension's fp16 knob (what "auto" precision resolves to) in step."""
+    global _fp16_pushed
+    want = config.ATTENTION_PRECISION in ("auto", "fp16")
+    if _fp16_pushed != want:
+        kernels.wmma_set_fp16(want)
+        _fp16_pushed = want
+
+
+def _sync_cp_async(kernels) -> None:
+    global _cp_async_pushed
+    want = config._CP_ASYNC_CODE[config.CP_ASYNC]
+    if _cp_async_pushed != want and hasattr(kernels, "wmma_set_cp_async"):
+        kernels.wmma_set_cp_async(want)
+        _cp_async_pushed = want
+
+
+def _custom_kernels():
+    """The extension object, or None when the library would not load."""
+    import kernel_ext
+
+    return kernel_ext.get_kernels()
+
+
+def _add_layernorm(x: torch.Tensor, sub: torch.Tensor, norm,
+                   normed_half: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(x + sub, norm(x + sub)) in one kernel."""
+    kernels = _custom_kernels()
+    if kernels is not None:
+        return tuple(kernels.fused_add_layernorm(x, sub, norm.weight, norm.bias, norm.eps,
+                                                 normed_half))
+    fallback_counts["add_layernorm"] += 1
+    total = x + sub
+    out = F.layer_norm(total, (total.shape[-1],), norm.weight, norm.bias, norm.eps)
+    return total, (out.half() if normed_half else out)
+
+
+def _linear_gelu(x: torch.Tensor, lin, out_half: bool = False) -> torch.Tensor:
+    """GELU_erf(lin(x)) with the GELU in the GEMM epilogue."""
+    if config.LINEAR_GELU != "off" and lin.bias is not None:
+        kernels = _custom_kernels()
+        if kernels is not None:
+            out = kernels.linear_gelu(x, lin.weight, lin.bias, -1,
+                                      config._GEMM_MATH_CODE[config.LINEAR_GELU], out_half)
+            if out is not None:
+                return out
+    fallback_counts["linear_gelu"] += 1
+    out = F.gelu(F.linear(x.to(lin.weight.dtype), lin.weight, lin.bias), approximate="none")
+    return out.half() if out_half else out
+
+
+def _layernorm(x: torch.Tensor, norm, out_half: bool = False) -> torch.Tensor:
+    """LayerNorm(x) * w + b: the model's one norm with no residual before it."""
+    if config.LAYERNORM != "off":
+        kernels = _custom_kernels()
+        if kernels is not None:
+            return kernels.fused_layernorm(x, norm.weight, norm.bias, norm.eps, out_half)
+    fallback_counts["layernorm"] += 1
+    out = F.layer_norm(x, (x.shape[-1],), norm.weight, norm.bias, norm.eps)
+    return out.half() if out_half else out
+
+
+def _attention_wants_fp16() -> bool:
+    """Will attention really contract q/k/v in fp16 (so fp16 q/k/v are free)?"""
+    if config.QKV_FP16 == "off":
+        return False
+    if config.ATTENTION_IMPL not in ("auto", "wmma"):
+        return False
+    return config.ATTENTION_PRECISION in ("auto", "fp16")
+
+
+def _qkv_math_code() -> int:
+    """linear_bias `math` for the QKV projection (config.QKV_PRECISION)."""
+    if config.LINEAR_BIAS == "tf32":
+        return config._GEMM_MATH_CODE["tf32"]
+    return config._QKV_MATH_CODE[config.QKV_PRECISION]
+
+
+def _normed_wants_fp16(rows: int, width: int) -> bool:
+    """Should a LayerNorm feeding the QKV projection emit fp16?
+
+    Only when that projection narrows its A operand to fp16 anyway: one-pass
+    fp16 math. The split fp16x3 projection needs the fp32 values.
+    """
+    if config.NORMED_FP16 == "off" or config.LINEAR_BIAS != "auto":
+        return False
+    if _qkv_math_code() != -1:
+        return False
+    if width > config._NORMED_FP16_MAX_K:
+        return False
+    return config._QKV_FP16_MIN_ROWS <= rows <= config._LINEAR_BIAS_MAX_ROWS
+
+
+def _gelu_input_wants_fp16(rows: int, width: int) -> bool:
+    """Should norm2 emit fp16 for linear_gelu (which narrows A with the same RNE)?"""
+    if config.NORMED_FP16 == "off" or config.LINEAR_GELU != "auto":
+        return False
+    if width > config._NORMED_FP16_MAX_K:
+        return False
+    return config._QKV_FP16_MIN_ROWS <= rows <= config._LINEAR_BIAS_MAX_ROWS
+
+
+def _gelu_output_wants_fp16(rows: int) -> bool:
+    """Should linear_gelu store fp16 for ffn_out (whose fp16 math narrows it anyway)?"""
+    if config.GELU_FP16 == "off" or config.LINEAR_BIAS != "auto":
+        return False
+    return rows <= config._LINEAR_BIAS_MAX_ROWS
+
+
+def _linear_bias(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
+                 out_half: bool = False, math: Optional[int] = None) -> torch.Tensor:
+    """x @ weight^T + bias on the MFMA GEMM; `math` overrides the config's."""
+    rows = x.numel() // x.shape[-1] if x.dim() >= 1 and x.shape[-1] else 0
+    if (config.LINEAR_BIAS != "off" and bias is not None
+            and rows <= config._LINEAR_BIAS_MAX_ROWS):
+        kernels = _custom_kernels()
+        if kernels is not None:
+            code = config._GEMM_MATH_CODE[config.LINEAR_BIAS] if math is None else math
+            out = kernels.linear_bias(x, weight, bias, -1, code, out_half)
+            if out is not None:
+                return out
+    fallback_counts["linear_bias"] += 1
+    out = F.linear(x.to(weight.dtype), weight, bias)
+    want = torch.float16 if out_half else torch.float32
+    return out if out.dtype == want else out.to(want)
+
+
+def _ffn_block(x, attn_out, norm1, ffn_in, ffn_out, norm2):
+    """The fused post-attention block, or None to run it unfused."""
+    if config.FFN_BLOCK == "off":
+        return None
+    if config.FFN_BLOCK != "force" and x.shape[-1] > config._FFN_BLOCK_MAX_D:
+        return None
+    kernels = _custom_kernels()
+    if kernels is None or not hasattr(kernels, "fused_ffn_block"):
+        return None
+    out = kernels.fused_ffn_block(x, attn_out, norm1.weight, norm1.bias, ffn_in.weight,
+                                  ffn_in.bias, ffn_out.weight, ffn_out.bias, norm2.weight,
+                                  norm2.bias, norm1.eps)
+    return (out[0], out[1]) if out else None
+
+
+def _attention_dispatch(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                        attn_mask: Optional[torch.Tensor], is_causal: bool,
+                        scale: float) -> torch.Tensor:
+    """Attention on the MFMA kernel; there is no other route.
+
+    Returns [B, S, H*head_dim]. `attn_mask` ([B,1,1,S] key mask, True = may
+    attend) and `is_causal` may both be set: causal stays a flag so the kernel
+    skips the tiles past the diagonal instead of masking them.
+    """
+    import kernel_ext
+
+    kernels = kernel_ext.get_kernels()
+    if kernels is None:
+        raise RuntimeError(
+            "the gfx950 extension (libdotl_hip.so) failed to load, and there is no "
+            "fallback: this project implements attention itself and will not substitute "
+            f"a prebuilt one. Cause: {kernel_ext.load_error()}")
+    _sync_attention_precision(kernels)
+    _sync_cp_async(kernels)
+    return kernels.fused_attention_forward(
+        q, k, v, attn_mask, is_causal, scale,
+        config._IMPL_CODE[config.ATTENTION_IMPL],
+        config._OUT_LAYOUT_BSHD,
+        config._PRECISION_CODE[config.ATTENTION_PRECISION],
+    )

@@ -1,0 +1,163 @@
+"""Drop-in replacements for the baseline's submodules (reference optimized/layers.py).
+
+Parameter and submodule names match BaselineTransformer's
+(torch_transformer_benchmark.py:70-245), so one state_dict loads into either
+model with strict=True: the parameter names are the weight format.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import config
+from .kernels import (_add_layernorm, _attention_dispatch, _attention_wants_fp16, _ffn_block,
+                      _gelu_input_wants_fp16, _gelu_output_wants_fp16, _layernorm,
+                      _linear_bias, _linear_gelu, _normed_wants_fp16, _qkv_math_code)
+from .util import _version_or_none
+
+
+class MyLinear(nn.Module):
+    """nn.Linear's parameter names and shapes (weight [out, in], bias [out])."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.empty(out_features, in_features))
+        self.bias = nn.Parameter(torch.empty(out_features)) if bias else None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        # out_proj and ffn_out; the QKV weights are fused in MySelfAttention and
+        # ffn_in goes through _linear_gelu.
+        return _linear_bias(x, self.weight, self.bias)
+
+
+class MyLayerNorm(nn.Module):
+    """nn.LayerNorm's parameter names and shapes."""
+
+    def __init__(self, d_model: int, eps: float = 1e-5) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(d_model))
+        self.bias = nn.Parameter(torch.zeros(d_model))
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        # Reached by the model's first norm (every other one is fused into a
+        # residual add) and by the padded path's trailing norm. Its consumer
+        # is a QKV projection, so it may narrow on the same terms.
+        rows = x.numel() // x.shape[-1]
+        return _layernorm(x, self, out_half=_normed_wants_fp16(rows, x.shape[-1]))
+
+
+class MySelfAttention(nn.Module):
+    """BaselineSelfAttention's submodule names (q_proj, k_proj, v_proj, out_proj)."""
+
+    def __init__(self, d_model: int, num_heads: int) -> None:
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = d_model // num_heads
+        self.scale = self.head_dim ** -0.5
+        self.q_proj = MyLinear(d_model, d_model)
+        self.k_proj = MyLinear(d_model, d_model)
+        self.v_proj = MyLinear(d_model, d_model)
+        self.out_proj = MyLinear(d_model, d_model)
+        # Fused [3D, D] QKV weight and [3D] bias, rebuilt when a source
+        # parameter moves (device/dtype) or changes (version). Plain
+        # attributes, so they stay out of state_dict().
+        self._qkv_key: Optional[Tuple] = None
+        self._qkv_weight: Optional[torch.Tensor] = None
+        self._qkv_bias: Optional[torch.Tensor] = None
+
+    def _get_qkv_weight(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Q, K and V projections as one [3*d_model, d_model] GEMM operand.
+
+        One GEMM with N = 3D instead of three with N = D: three times the
+        output tiles per launch, one read of the normalised input instead of
+        three (reference optimized/layers.py:88-110 does the same for its card).
+        """
+        wq, wk, wv = self.q_proj.weight, self.k_proj.weight, self.v_proj.weight
+        key = (wq.device, wq.dtype, _version_or_none(wq), _version_or_none(wk),
+               _version_or_none(wv), _version_or_none(self.q_proj.bias),
+               _version_or_none(self.k_proj.bias), _version_or_none(self.v_proj.bias))
+        if self._qkv_key != key:
+            with torch.no_grad():
+                self._qkv_weight = torch.cat([wq, wk, wv], dim=0)
+                self._qkv_bias = torch.cat([self.q_proj.bias, self.k_proj.bias,
+                                            self.v_proj.bias], dim=0)
+            self._qkv_key = key
+        return self._qkv_weight, self._qkv_bias
+
+    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,
+                causal: bool = False, mask_is_trivial: bool = False) -> torch.Tensor:
+        batch, seq_len, _ = x.shape
+        qkv_w, qkv_b = self._get_qkv_weight()
+        rows = batch * seq_len
+        # fp16 q/k/v when attention contracts in fp16: the projection's
+        # epilogue applies the RNE attention would apply while staging.
+        want_half = (_attention_wants_fp16()
+                     and config._QKV_FP16_MIN_ROWS <= rows <= config._LINEAR_BIAS_MAX_ROWS)
+        qkv = _linear_bias(x, qkv_w, qkv_b, out_half=want_half, math=_qkv_math_code())
+        # [B, S, 3, H, hd] -> three strided [B, H, S, hd] views; no copies.
+        q, k, v = (qkv.view(batch, seq_len, 3, self.num_heads, self.head_dim)
+                   .permute(2, 0, 3, 1, 4).unbind(0))
+
+        use_mask = valid_token_mask is not None and not mask_is_trivial
+        # Key padding stays a [B, 1, 1, S] mask and causal stays a flag.
+        attn_mask = valid_token_mask[:, None, None, :] if use_mask else None
+        context = _attention_dispatch(q, k, v, attn_mask=attn_mask, is_causal=causal,
+                                      scale=self.scale)
+        output = self.out_proj(context)
+        if use_mask:
+            output = output.masked_fill(~valid_token_mask[..., None], 0)
+        return output
+
+
+class MyTransformerBlock(nn.Module):
+    """BaselineTransformerBlock's submodule names (norm1, attention, norm2, ffn_in, ffn_out)."""
+
+    def __init__(self, d_model: int, num_heads: int, ffn_dim: int, causal: bool) -> None:
+        super().__init__()
+        self.norm1 = MyLayerNorm(d_model)
+        self.attention = MySelfAttention(d_model, num_heads)
+        self.norm2 = MyLayerNorm(d_model)
+        self.ffn_in = MyLinear(d_model, ffn_dim)
+        self.ffn_out = MyLinear(ffn_dim, d_model)
+        self.causal = causal
+
+    def forward(self, x: torch.Tensor, normed: torch.Tensor, next_norm: "MyLayerNorm",
+                valid_token_mask: Optional[torch.Tensor] = None, mask_is_trivial: bool = False,
+                next_norm_is_output: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Returns (residual stream, next_norm applied to it).
+
+        `normed` is norm1(x), computed by whoever produced x; `next_norm` is
+        the LayerNorm that consumes this block's output (the next block's
+        norm1, or final_norm), so both residual adds fuse with a norm.
+        """
+        attn_out = self.attention(normed, valid_token_mask, self.causal, mask_is_trivial)
+        use_mask = valid_token_mask is not None and not mask_is_trivial
+
+        if not use_mask:
+            fused = _ffn_block(x, attn_out, self.norm2, self.ffn_in, self.ffn_out, next_norm)
+            if fused is not None:
+                return fused
+
+        rows = x.numel() // x.shape[-1]
+        x, normed = _add_layernorm(x, attn_out, self.norm2,
+                                   normed_half=_gelu_input_wants_fp16(rows, x.shape[-1]))
+        hidden = _linear_gelu(normed, self.ffn_in, out_half=_gelu_output_wants_fp16(rows))
+        ffn_out = self.ffn_out(hidden)
+
+        if use_mask:
+            # The reference zeroes padded rows between the add and the norm.
+            x = (x + ffn_out).masked_fill(~valid_token_mask[..., None], 0)
+            return x, next_norm(x) if not next_norm_is_output else _final_norm(x, next_norm)
+
+        trailing_half = (not next_norm_is_output
+                         and _normed_wants_fp16(rows, x.shape[-1]))
+        return _add_layernorm(x, ffn_out, next_norm, normed_half=trailing_half)
+
+
+def _final_norm(x: torch.Tensor, norm: "MyLayerNorm") -> torch.Tensor:
+    """The model's output norm: never narrowed."""
+    return _layernorm(x, norm, out_half=False)

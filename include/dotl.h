@@ -1,0 +1,186 @@
+/*
+ * dotl.h -- C ABI of libdotl_hip.so, the MI355X (gfx950) kernels behind the
+ * single-transformer-layer forward pass.
+ *
+ * This is the drop-in boundary for the reference's pybind module
+ * `transformer_kernels` (reference csrc/fused_attention.cu:118-376). Every
+ * entry point below replaces one pybind entry; the Python shim
+ * (kernel_ext.py in the package source root) rebuilds the reference's
+ * torch-level signatures on top of these, so optimized/kernels.py calls the
+ * same names with the same arguments.
+ *
+ * Conventions
+ *   - Plain device pointers, int64 sizes and strides in ELEMENTS, a dtype
+ *     code, and the HIP stream to launch on (hipStream_t passed as void*;
+ *     NULL is the default stream). Nothing here allocates device memory:
+ *     outputs and workspace are the caller's, so every entry point is legal
+ *     inside hipGraph stream capture.
+ *   - Return value: DOTL_OK (0) after launching, DOTL_DECLINED (1) when the
+ *     case is outside what the kernels cover and nothing was launched (the
+ *     caller picks a fallback, as the reference's undefined-tensor / empty-list
+ *     returns do), and a negative DOTL_E_* code on error, with a message in
+ *     dotl_last_error() (thread-local, valid until the next call on the same
+ *     thread). Negative codes correspond to the reference's TORCH_CHECK raises.
+ *   - Launches are asynchronous on `stream`; hipGetLastError is checked after
+ *     every launch.
+ *   - Load the library only after the process's HIP runtime is up (import
+ *     torch first): it binds to the libamdhip64 already loaded.
+ */
+#ifndef DOTL_H
+#define DOTL_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DOTL_ABI_VERSION 1
+
+#define DOTL_OK 0
+#define DOTL_DECLINED 1
+#define DOTL_E_INVALID (-1)   /* bad argument: the reference's TORCH_CHECK raise */
+#define DOTL_E_LAUNCH (-2)    /* hipGetLastError reported a failure */
+#define DOTL_E_UNSUPPORTED (-3) /* a forced impl/precision that does not exist */
+
+/* dtype codes */
+#define DOTL_F32 0
+#define DOTL_F16 1
+
+/* linear activation codes */
+#define DOTL_ACT_NONE 0
+#define DOTL_ACT_GELU 1 /* exact erf GELU, F.gelu(approximate="none") */
+
+/* linear math codes (the reference's `math` argument: -1 auto, 0 tf32,
+ * reference csrc/linear_gelu.cuh:598-719) */
+#define DOTL_MATH_FP16 0   /* fp16 operands, fp32 accumulate: one MFMA pass */
+#define DOTL_MATH_FP16X3 1 /* split fp16 hi+lo operands, three MFMA passes:
+                              fp32-class products (the reference's tf32 slot) */
+
+/* Thread-local message for the last negative return; "" if none. */
+const char* dotl_last_error(void);
+
+/* DOTL_ABI_VERSION of the loaded library. */
+int dotl_abi_version(void);
+
+/* Name of the device the library was built for ("gfx950"). */
+const char* dotl_target(void);
+
+/* y[i] = x[i] for i < n (float32). Replaces smoke_test_identity
+ * (reference csrc/fused_attention.cu:96-114). */
+int dotl_smoke_test_identity(const float* x, float* y, int64_t n, void* stream);
+
+/* Writes the accumulator (row, col) that each (lane, register) of one
+ * v_mfma_f32_32x32x16_f16 and one v_mfma_f32_16x16x32_f16 holds, as
+ * out[0 .. 64*16) = row*32+col for 32x32, then out[1024 .. 1024+64*4) =
+ * row*16+col for 16x16 (int32 device buffer, 1280 elements). The MFMA
+ * counterpart of the reference's accumulator probe (acc_row_probe_kernel,
+ * reference csrc/attention_wmma.cuh:798-828), run as a test, not at start-up. */
+int dotl_mfma_layout_probe(int32_t* out, void* stream);
+
+/*
+ * LayerNorm over the last dimension, optionally fused with a residual add.
+ * Replaces fused_add_layernorm / fused_layernorm
+ * (reference csrc/add_layernorm.cuh:491-692).
+ *
+ *   x, sub      [rows, D] contiguous, dtype DOTL_F32. sub == NULL: plain LN.
+ *   weight,bias [D] float32
+ *   x_new       [rows, D] float32 output, x + sub (rounded to fp32); may be
+ *               NULL to skip the store (required NULL when sub == NULL)
+ *   normed      [rows, D] output of dtype normed_dtype (DOTL_F32 or DOTL_F16,
+ *               RNE narrowing), LayerNorm(x + sub) * weight + bias
+ *   Statistics: fp32, mean then the centred sum of squares (biased variance),
+ *   eps inside the square root.
+ *   D in [1, 8192]; rows >= 0.
+ */
+int dotl_layernorm(const void* x, const void* sub, const float* weight, const float* bias,
+                   void* x_new, void* normed, int64_t rows, int64_t D, double eps,
+                   int dtype, int normed_dtype, void* stream);
+
+/*
+ * Weight preparation for dotl_linear: w_hi = fp16(w) (RNE) and, when w_lo is
+ * not NULL, w_lo = fp16((w - w_hi) * 2^12), the scaled residual the
+ * DOTL_MATH_FP16X3 path consumes. n elements, float32 in.
+ * No reference counterpart of its own: the reference narrows W inside the
+ * GEMM's staging (reference csrc/linear_gelu.cuh:186-462); here the narrowing
+ * is done once per weight version and cached by the caller.
+ */
+int dotl_weight_split(const float* w, void* w_hi, void* w_lo, int64_t n, void* stream);
+
+/*
+ * out[M, N] = act(x[M, K] @ W[N, K]^T + bias[N]) on MFMA.
+ * Replaces linear_bias / linear_gelu (reference csrc/linear_gelu.cuh:598-756).
+ *
+ *   x         [M, K] contiguous, x_dtype DOTL_F32 (narrowed with RNE when
+ *             staged) or DOTL_F16
+ *   w_hi      [N, K] fp16 from dotl_weight_split
+ *   w_lo      [N, K] fp16 scaled residual; required for DOTL_MATH_FP16X3
+ *   bias      [N] float32 (required; the reference's kernels always add one)
+ *   out       [M, N], out_dtype DOTL_F32 or DOTL_F16 (RNE)
+ *   act       DOTL_ACT_NONE / DOTL_ACT_GELU, applied in fp32 before the store
+ *   math      DOTL_MATH_FP16 or DOTL_MATH_FP16X3 (an fp16 x is exact in
+ *             fp16, so with it the split path runs two passes: x*hi + x*lo)
+ *   tile      -1 auto; otherwise a tile id (0: 128x128, 1: 256x128, 2: 64x64)
+ *   Declines when K % 8 != 0.
+ */
+int dotl_linear(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
+                const float* bias, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                int act, int math, int tile, void* stream);
+
+/*
+ * Fused scaled-dot-product attention, flash style on MFMA.
+ * Replaces fused_attention_forward
+ * (reference csrc/attention_dispatch.cuh:332-519).
+ *
+ *   q, k, v      logical [B, H, S, head_dim], dtype DOTL_F16 or DOTL_F32
+ *                (narrowed with RNE when staged), head_dim stride 1, and
+ *                the (batch, head, seq) strides given once in qkv_strides[3]
+ *                (in elements) for all three -- the strided views of a fused
+ *                [B, S, 3, H, hd] projection pass through without copies.
+ *   mask         optional (NULL) bool bytes, true = may attend, addressed as
+ *                mask[b*ms[0] + h*ms[1] + i*ms[2] + j*ms[3]] (expanded
+ *                [B,H,S,S] strides; stride 0 on broadcast dims)
+ *   out          out_layout 0: [B, H, S, head_dim]; 1: [B, S, H*head_dim];
+ *                dtype out_dtype (DOTL_F16 or DOTL_F32)
+ *   is_causal    key j > query i is excluded (combinable with mask)
+ *   impl         0 auto, 1 scalar, 2 wmma (here: the MFMA kernel), 3 tile
+ *   precision    0 auto, 1 fp32, 2 tf32, 3 fp16, 4 bf16
+ *   A query row with no allowed key produces 0.
+ *   Returns DOTL_DECLINED when no kernel covers (dtype, head_dim); the caller
+ *   raises, as the reference does.
+ */
+int dotl_attention_forward(const void* q, const void* k, const void* v, int dtype,
+                           const int64_t* qkv_strides, const uint8_t* mask,
+                           const int64_t* mask_strides, void* out, int out_dtype,
+                           int out_layout, int B, int H, int S, int head_dim,
+                           int is_causal, double scale, int impl, int precision,
+                           void* stream);
+
+/*
+ * Fused post-attention block (add+LN, Linear+GELU, Linear, add+LN).
+ * Replaces fused_ffn_block (reference csrc/ffn_block.cuh:270-311), whose
+ * contract is "run it or decline": this build declines every shape
+ * (DOTL_DECLINED), and the caller runs the unfused chain -- which the
+ * reference's own gate also does at every configured width above 64.
+ */
+int dotl_ffn_block(const float* x, const float* attn_out, const float* norm1_w,
+                   const float* norm1_b, const float* ffn_in_w, const float* ffn_in_b,
+                   const float* ffn_out_w, const float* ffn_out_b, const float* norm2_w,
+                   const float* norm2_b, float* x_out, float* normed_out, int64_t rows,
+                   int64_t D, int64_t F, double eps, void* stream);
+
+/* Process-wide knobs with the reference's names
+ * (reference csrc/fused_attention.cu:234-339). wmma_set_fp16 selects the
+ * arithmetic "auto" attention precision resolves to: fp16 (1) or the split
+ * fp16x3 path (0). cp_async has no gfx950 meaning; it is accepted and
+ * remembered so callers that push it keep working. */
+void dotl_wmma_set_fp16(int on);
+int dotl_wmma_fp16(void);
+void dotl_wmma_set_cp_async(int mode);
+int dotl_wmma_cp_async_mode(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DOTL_H */
