@@ -166,15 +166,21 @@ def test_gemm_half_output_is_rne_of_fp32(kernels):
     f16 = kernels.linear_bias(_t(x), _t(w), _t(b), -1, -1, True)
     assert f16.dtype == torch.float16
     assert torch.equal(f16, f32.half())
+    # The GELU epilogue of the two instantiations may contract its multiply-adds
+    # differently (<= 1 fp32 ulp apart), which can flip a tie in the fp16
+    # rounding: allow one fp16 ulp.
     g32 = kernels.linear_gelu(_t(x), _t(w), _t(b), -1, -1, False)
     g16 = kernels.linear_gelu(_t(x), _t(w), _t(b), -1, -1, True)
-    assert torch.equal(g16, g32.half())
+    ref16 = g32.half().float()
+    ulp = torch.from_numpy(np.spacing(np.abs(ref16.cpu().numpy()).astype(np.float16))).float()
+    assert torch.all((g16.float() - ref16).abs().cpu() <= ulp)
 
 
 def test_gemm_declines_uncovered(kernels):
     x, w, b = _gemm_case(16, 16, 12, 1)
     assert kernels.linear_bias(_t(x), _t(w), _t(b)) is None
-    assert kernels.linear_bias(_t(x).double(), _t(w[:, :8]).double(), _t(b).double()) is None
+    x8, w8, b8 = _gemm_case(16, 16, 8, 1)
+    assert kernels.linear_bias(_t(x8).double(), _t(w8).double(), _t(b8).double()) is None
 
 
 def test_gemm_weight_cache_follows_in_place_updates(kernels):
@@ -304,8 +310,7 @@ def test_attention_general_mask(kernels):
     r = np.random.default_rng(1)
     m = r.random((B, 1, S, S)) < 0.7
     m[:, :, :, 0] = True
-    want = reference_attention(_h(q), _h(k), _h(v), None, False, 0.2, dtype=torch.float64)
-    # apply the general mask in the fp64 reference directly
+    # the general mask applied in an fp64 reference directly
     qd, kd, vd = (torch.from_numpy(_h(a)) for a in (q, k, v))
     s = (qd @ kd.transpose(-1, -2)) * 0.2
     s = s.masked_fill(~torch.from_numpy(m), float("-inf"))
