@@ -80,6 +80,39 @@ def time_layer(model, x, mask, steps, warmup):
     return (t1 - t0) * 1000.0 / steps
 
 
+def device_us(fn, reps, replays=5):
+    """Device time of one call of `fn`, in microseconds.
+
+    `reps` back-to-back calls are captured into one hipGraph and the graph is
+    replayed between two HIP events on the capture stream, so host launch
+    overhead (Python, ctypes) does not pad short kernels.
+    """
+    import torch
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    stream = torch.cuda.current_stream()
+    start.record(stream)
+    for _ in range(replays):
+        g.replay()
+    end.record(stream)
+    end.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / (reps * replays)
+    g.reset()
+    return us
+
+
 def kernel_table(cfg, model, x, mask, reps):
     """Time each kernel of the layer alone (HIP events on the launch stream).
 
@@ -88,7 +121,6 @@ def kernel_table(cfg, model, x, mask, reps):
     import torch
 
     import kernel_ext
-    from optimized import kernels as ok
     from oracle.inputs import attention_useful_flops, lengths_of
 
     kx = kernel_ext.get_kernels()
@@ -103,9 +135,9 @@ def kernel_table(cfg, model, x, mask, reps):
 
     with torch.inference_mode():
         x2 = x.reshape(T, D)
-        normed32 = kx.fused_layernorm(x2, layer.norm1.weight, layer.norm1.bias)
+        planes = kx.fused_layernorm_split(x2, layer.norm1.weight, layer.norm1.bias)
         qkv_w, qkv_b = attn._get_qkv_weight()
-        qkv = kx.linear_bias(normed32, qkv_w, qkv_b, -1, ok._qkv_math_code(), True)
+        qkv = kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True)
         q, k, v = qkv.view(B, S, 3, H, hd).permute(2, 0, 3, 1, 4).unbind(0)
         amask = None if mask is None else mask[:, None, None, :]
         ctx = kx.fused_attention_forward(q, k, v, amask, cfg.causal, hd ** -0.5, 0, 1, 0)
@@ -117,11 +149,11 @@ def kernel_table(cfg, model, x, mask, reps):
         ffn = kx.linear_bias(hidden, layer.ffn_out.weight, layer.ffn_out.bias)
 
         ops = {
-            "layernorm (norm1, fp32 out)": (
-                lambda: kx.fused_layernorm(x2, layer.norm1.weight, layer.norm1.bias),
+            "layernorm (norm1, split-fp16 out)": (
+                lambda: kx.fused_layernorm_split(x2, layer.norm1.weight, layer.norm1.bias),
                 "hbm", T * D * 8.0),
             "linear qkv (fp16x3, fp16 out)": (
-                lambda: kx.linear_bias(normed32, qkv_w, qkv_b, -1, ok._qkv_math_code(), True),
+                lambda: kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True),
                 "mfma", 2.0 * T * D * 3 * D),
             "attention": (
                 lambda: kx.fused_attention_forward(q, k, v, amask, cfg.causal, hd ** -0.5, 0, 1, 0),
@@ -145,18 +177,8 @@ def kernel_table(cfg, model, x, mask, reps):
                 "hbm", T * D * 16.0),
         }
         out = {}
-        stream = torch.cuda.current_stream(dev)
         for name, (fn, bound, work) in ops.items():
-            for _ in range(3):
-                fn()
-            start = torch.cuda.Event(enable_timing=True)
-            end = torch.cuda.Event(enable_timing=True)
-            start.record(stream)
-            for _ in range(reps):
-                fn()
-            end.record(stream)
-            end.synchronize()
-            us = start.elapsed_time(end) * 1000.0 / reps
+            us = device_us(fn, reps)
             if bound == "mfma":
                 achieved = work / (us * 1e-6) / 1e12
                 out[name] = dict(us=us, flops=work, bound="mfma", achieved=achieved,
@@ -224,7 +246,7 @@ def run_config(name, steps, warmup, graph, with_kernels=True):
                params=params, ms=ms, ms_eager=ms_eager, flops=flops,
                graphs=len(model._graphs))
     if with_kernels:
-        res["kernels"] = kernel_table(cfg, model, x, mask, max(10, steps))
+        res["kernels"] = kernel_table(cfg, model, x, mask, 20)
     return res
 
 

@@ -33,14 +33,10 @@ __global__ void identity_kernel(const float* __restrict__ x, float* __restrict__
     if (i < n) y[i] = x[i];
 }
 
-// One wavefront. Operand A row i carries a one-hot of i across k, operand B
-// column j carries (j + 1) at k == that one-hot: C[i][j] = (j + 1) * [k match].
-// Chosen so each accumulator element encodes its own (row, col):
-//   A[i][k] = (k == i % K) ? 1 : 0 ... not unique for rows >= K, so instead
-// the probe runs the MFMA with A[i][k] = i + 1 at k == 0 only and
-// B[k][j] = 1 at k == 0 only, giving C[i][j] = i + 1, then a second MFMA with
-// A[i][0] = 1 and B[0][j] = j + 1, giving C[i][j] = j + 1. Both are exact in
-// fp16/fp32 for i, j < 32.
+// One wavefront. Two MFMAs per instruction shape, each with a single nonzero
+// K slot (lane group 0, element 0): A[i][0] = i + 1 against B[0][j] = 1 gives
+// C[i][j] = i + 1, and A[i][0] = 1 against B[0][j] = j + 1 gives j + 1, so
+// every accumulator register reports its own (row, col). Exact for i, j < 32.
 __global__ void mfma_probe_kernel(int32_t* out) {
     const int lane = threadIdx.x;
     // 32x32x16: lane supplies A[l % 32][8 * (l / 32) + e] and B[8 * (l / 32) + e][l % 32].
@@ -83,6 +79,22 @@ __global__ void mfma_probe_kernel(int32_t* out) {
     }
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// One wave: zero a 2 KiB LDS region, DMA 16 bytes per lane into its start,
+// copy the region out.
+__global__ void lds_dma_probe_kernel(const int32_t* __restrict__ src, int32_t* __restrict__ out) {
+    __shared__ __attribute__((aligned(1024))) int32_t region[512];
+    const int lane = threadIdx.x;
+    for (int i = lane; i < 512; i += 64) region[i] = 0;
+    __syncthreads();
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + 4 * lane),
+                                     (lds_void_t*)(region), 16, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int i = lane; i < 512; i += 64) out[i] = region[i];
+}
+
 }  // namespace
 }  // namespace dotl
 
@@ -113,6 +125,14 @@ int dotl_mfma_layout_probe(int32_t* out, void* stream) {
     DOTL_REQUIRE(out != nullptr, "mfma_layout_probe: null output");
     hipLaunchKernelGGL(dotl::mfma_probe_kernel, dim3(1), dim3(64), 0, dotl::as_stream(stream), out);
     return dotl::check_launch("mfma_layout_probe");
+}
+
+int dotl_lds_dma_probe(const int32_t* src, int32_t* out, void* stream) {
+    dotl::clear_error();
+    DOTL_REQUIRE(src != nullptr && out != nullptr, "lds_dma_probe: null pointer");
+    hipLaunchKernelGGL(dotl::lds_dma_probe_kernel, dim3(1), dim3(64), 0, dotl::as_stream(stream),
+                       src, out);
+    return dotl::check_launch("lds_dma_probe");
 }
 
 void dotl_wmma_set_fp16(int on) { dotl::g_wmma_fp16.store(on ? 1 : 0); }

@@ -59,9 +59,27 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// Exact GELU, 0.5 x (1 + erf(x / sqrt 2)), with the device library's erff.
+// erf GELU, 0.5 x (1 + erf(x / sqrt 2)), with erf from Abramowitz &
+// Stegun, Handbook of Mathematical Functions, formula 7.1.26:
+//   erfc(z) ~= (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),
+//   t = 1 / (1 + p z), z >= 0, |error in erf| <= 1.5e-7.
+// Written on erfc so neither sign cancels: with z = |x| / sqrt 2 and
+// q = erfc(z), GELU(x) = x - x q / 2 for x >= 0 and x q / 2 for x < 0.
+// One reciprocal, one exp2 and seven FMAs; the device library's erff costs
+// several times that, and an epilogue that applies it to every output of a
+// GEMM with a short K spends more time there than in the MFMAs.
 __device__ __forceinline__ float gelu_erf(float x) {
-    return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+    const float z = fabsf(x) * 0.70710678118654752440f;
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+    float poly = fmaf(1.061405429f, t, -1.453152027f);
+    poly = fmaf(poly, t, 1.421413741f);
+    poly = fmaf(poly, t, -0.284496736f);
+    poly = fmaf(poly, t, 0.254829592f);
+    poly *= t;
+    // exp(-z^2) = exp2(-z^2 log2 e)
+    const float q = poly * __builtin_amdgcn_exp2f(-z * z * 1.44269504088896341f);
+    const float h = q == 0.f ? 0.f : 0.5f * x * q;  // q == 0 at |x| = inf
+    return x >= 0.f ? x - h : h;
 }
 
 // fp32 -> fp16 with round-to-nearest-even (the hardware conversion).

@@ -12,9 +12,12 @@
 //     [rows][BK] and every fragment is one 16-byte LDS read;
 //   * 256 threads = 4 wavefronts in a 2 x 2 grid, each wavefront owning a
 //     (BM/2) x (BN/2) block of 32x32 accumulator tiles;
-//   * the next K tile is fetched from HBM into registers while the current
-//     one is multiplied out of LDS (register double buffering), so the LDS
-//     footprint is one tile and several workgroups fit per CU;
+//   * a two-stage pipeline: while the MFMAs read K tile kt from one LDS
+//     stage, tile kt+1 (already in registers) is written to the other stage
+//     and tile kt+2 is in flight from HBM/L2 -- one barrier per K step;
+//   * a tile menu from 64x64 to 256x256 (the 256x256 tile holds a 128x128
+//     accumulator block per wavefront: 256 accumulator registers), picked
+//     per shape so the grid covers the 256 CUs;
 //   * LDS rows are padded by 16 bytes so the 32 rows a fragment read touches
 //     fall on distinct bank groups;
 //   * W arrives pre-narrowed (dotl_weight_split, once per weight version);
@@ -32,6 +35,12 @@
 #include "dotl_common.h"
 
 namespace dotl {
+
+int pick_dma_tile(int64_t M, int64_t N, int passes);
+bool launch_gemm_dma(const _Float16* A, const _Float16* Alo, const _Float16* W,
+                     const _Float16* Wlo, const float* bias, void* C, int64_t M, int64_t N,
+                     int64_t K, int passes, int act, bool out_f16, int tile, hipStream_t stream);
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -158,18 +167,32 @@ __device__ __forceinline__ void tile_of(int64_t id, int64_t nm, int64_t nn, int6
     nt = r / gsize;
 }
 
+// LDS footprint of one pipeline stage, in halves: A [BM][LDK], W [BN][LDK],
+// and for the split path lo(W) [BN][LDK] and, with an fp32 A, lo(A) [BM][LDK].
+template <int BM, int BN, int BK, bool A_F32, bool SPLIT>
+struct StageLayout {
+    static constexpr int LDK = BK + kPad;
+    static constexpr int A = 0;
+    static constexpr int W = A + BM * LDK;
+    static constexpr int WLO = W + BN * LDK;
+    static constexpr int ALO = WLO + (SPLIT ? BN * LDK : 0);
+    static constexpr int SIZE = ALO + ((SPLIT && A_F32) ? BM * LDK : 0);
+    static constexpr size_t BYTES = 2u * SIZE * sizeof(_Float16);  // two stages
+};
+
 template <int BM, int BN, int BK, bool A_F32, bool SPLIT, int ACT, bool OUT_F16>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(
     const void* __restrict__ A_, const _Float16* __restrict__ Whi,
     const _Float16* __restrict__ Wlo, const float* __restrict__ bias,
     void* __restrict__ C_, int64_t M, int64_t N, int64_t K) {
     using TS = TileShape<BM, BN, BK>;
+    using SL = StageLayout<BM, BN, BK, A_F32, SPLIT>;
     constexpr int LDK = TS::LDK;
 
-    __shared__ __attribute__((aligned(16))) _Float16 sA[BM * LDK];
-    __shared__ __attribute__((aligned(16))) _Float16 sW[BN * LDK];
-    __shared__ __attribute__((aligned(16))) _Float16 sAlo[(SPLIT && A_F32) ? BM * LDK : 8];
-    __shared__ __attribute__((aligned(16))) _Float16 sWlo[SPLIT ? BN * LDK : 8];
+    // Two pipeline stages: while the MFMAs read stage kt&1, the next K tile
+    // (already in registers) is written to the other stage, and the tile after
+    // that is in flight from HBM/L2. One barrier per K step.
+    extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -198,37 +221,46 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
     HalfTile<BN, BK> tw;
     HalfTile<SPLIT ? BN : 8, SPLIT ? BK : 8> twlo;
 
-    const int64_t nk = (K + BK - 1) / BK;
-    if constexpr (A_F32) {
-        ta.load(static_cast<const float*>(A_), K, m0, M, 0, K);
-    } else {
-        ta.load(static_cast<const _Float16*>(A_), K, m0, M, 0, K);
+    auto fetch = [&](int64_t k0) {
+        if constexpr (A_F32) {
+            ta.load(static_cast<const float*>(A_), K, m0, M, k0, K);
+        } else {
+            ta.load(static_cast<const _Float16*>(A_), K, m0, M, k0, K);
+        }
+        tw.load(Whi, K, n0, N, k0, K);
+        if constexpr (SPLIT) twlo.load(Wlo, K, n0, N, k0, K);
+    };
+    auto commit = [&](_Float16* st) {
+        if constexpr (SPLIT && A_F32) {
+            ta.store_split(st + SL::A, st + SL::ALO);
+        } else {
+            ta.store(st + SL::A);
+        }
+        tw.store(st + SL::W);
+        if constexpr (SPLIT) twlo.store(st + SL::WLO);
+    };
+
+    // Bias columns for the epilogue, fetched before the K loop.
+    float bvals[TS::TN];
+#pragma unroll
+    for (int j = 0; j < TS::TN; ++j) {
+        const int64_t col = n0 + wn * TS::WN + j * 32 + lr;
+        bvals[j] = col < N ? bias[col] : 0.f;
     }
-    tw.load(Whi, K, n0, N, 0, K);
-    if constexpr (SPLIT) twlo.load(Wlo, K, n0, N, 0, K);
+
+    const int64_t nk = (K + BK - 1) / BK;
+    fetch(0);
+    commit(smem);
+    if (nk > 1) fetch(BK);
+    __syncthreads();
 
     for (int64_t kt = 0; kt < nk; ++kt) {
-        __syncthreads();  // previous tile's fragment reads are done
-        if constexpr (SPLIT && A_F32) {
-            ta.store_split(sA, sAlo);
-        } else {
-            ta.store(sA);
-        }
-        if constexpr (SPLIT) twlo.store(sWlo);
-        tw.store(sW);
-        __syncthreads();
+        _Float16* cur = smem + (kt & 1) * SL::SIZE;
+        if (kt + 1 < nk) commit(smem + ((kt + 1) & 1) * SL::SIZE);
+        if (kt + 2 < nk) fetch((kt + 2) * BK);
 
-        if (kt + 1 < nk) {
-            const int64_t k1 = (kt + 1) * BK;
-            if constexpr (A_F32) {
-                ta.load(static_cast<const float*>(A_), K, m0, M, k1, K);
-            } else {
-                ta.load(static_cast<const _Float16*>(A_), K, m0, M, k1, K);
-            }
-            tw.load(Whi, K, n0, N, k1, K);
-            if constexpr (SPLIT) twlo.load(Wlo, K, n0, N, k1, K);
-        }
-
+        const _Float16* sA = cur + SL::A;
+        const _Float16* sW = cur + SL::W;
 #pragma unroll
         for (int ks = 0; ks < TS::KS; ++ks) {
             const int kc = ks * 16 + lg * 8;
@@ -247,6 +279,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
             if constexpr (SPLIT) {
                 // 2^-12-scaled residual products: hi(x) * lo(W), and for an
                 // fp32 x also lo(x) * hi(W). An fp16 x has no residual.
+                const _Float16* sWlo = cur + SL::WLO;
                 half8 bl[TS::TN];
 #pragma unroll
                 for (int j = 0; j < TS::TN; ++j)
@@ -257,6 +290,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
                     for (int j = 0; j < TS::TN; ++j)
                         acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl[j], acc2[i][j], 0, 0, 0);
                 if constexpr (A_F32) {
+                    const _Float16* sAlo = cur + SL::ALO;
                     half8 al[TS::TM];
 #pragma unroll
                     for (int i = 0; i < TS::TM; ++i)
@@ -269,6 +303,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
                 }
             }
         }
+        __syncthreads();
     }
 
     // Epilogue. Accumulator register r of a 32x32 tile at lane l holds
@@ -277,7 +312,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
     for (int j = 0; j < TS::TN; ++j) {
         const int64_t col = n0 + wn * TS::WN + j * 32 + lr;
         if (col >= N) continue;
-        const float bcol = bias[col];
+        const float bcol = bvals[j];
 #pragma unroll
         for (int i = 0; i < TS::TM; ++i) {
 #pragma unroll
@@ -321,36 +356,59 @@ struct GemmArgs {
 
 template <int BM, int BN, int BK, bool A_F32, bool SPLIT, int ACT, bool OUT_F16>
 void launch(const GemmArgs& g) {
+    using SL = StageLayout<BM, BN, BK, A_F32, SPLIT>;
+    auto kern = gemm_kernel<BM, BN, BK, A_F32, SPLIT, ACT, OUT_F16>;
+    // Above 64 KiB of dynamic LDS the kernel must opt in; done once per
+    // instantiation, on the first (eager, never captured) call.
+    static const bool attr_ok = [&] {
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   static_cast<int>(SL::BYTES)) == hipSuccess;
+    }();
+    (void)attr_ok;
     const dim3 grid(static_cast<unsigned>(((g.N + BN - 1) / BN) * ((g.M + BM - 1) / BM)));
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, A_F32, SPLIT, ACT, OUT_F16>), grid,
-                       dim3(kThreads), 0, g.stream, g.A, g.Whi, g.Wlo, g.bias, g.C, g.M, g.N,
-                       g.K);
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), SL::BYTES, g.stream, g.A, g.Whi, g.Wlo, g.bias,
+                       g.C, g.M, g.N, g.K);
 }
 
+// Tile menu (ids are the C ABI's `tile` argument). 2 x 2 wavefronts each.
+//   0: 128 x 128   1: 256 x 128   2: 64 x 64   3: 256 x 256   4: 128 x 64
 template <bool A_F32, bool SPLIT, int ACT, bool OUT_F16>
-void launch_tile(const GemmArgs& g, int tile) {
+bool launch_tile(const GemmArgs& g, int tile) {
     switch (tile) {
-        case 2: launch<64, 64, 64, A_F32, SPLIT, ACT, OUT_F16>(g); break;
-        default: launch<128, 128, 64, A_F32, SPLIT, ACT, OUT_F16>(g); break;
+        case 0: launch<128, 128, 64, A_F32, SPLIT, ACT, OUT_F16>(g); return true;
+        case 2: launch<64, 64, 64, A_F32, SPLIT, ACT, OUT_F16>(g); return true;
+        case 4: launch<128, 64, 64, A_F32, SPLIT, ACT, OUT_F16>(g); return true;
+        case 1:
+            if constexpr (!SPLIT) { launch<256, 128, 64, A_F32, SPLIT, ACT, OUT_F16>(g); return true; }
+            return false;
+        case 3:
+            if constexpr (!SPLIT && !A_F32) { launch<256, 256, 64, A_F32, SPLIT, ACT, OUT_F16>(g); return true; }
+            return false;
     }
+    return false;
 }
 
 template <bool A_F32, bool SPLIT>
-void launch_epilogue(const GemmArgs& g, int tile, int act, bool out_f16) {
+bool launch_epilogue(const GemmArgs& g, int tile, int act, bool out_f16) {
     if (act == DOTL_ACT_GELU) {
-        out_f16 ? launch_tile<A_F32, SPLIT, DOTL_ACT_GELU, true>(g, tile)
-                : launch_tile<A_F32, SPLIT, DOTL_ACT_GELU, false>(g, tile);
-    } else {
-        out_f16 ? launch_tile<A_F32, SPLIT, DOTL_ACT_NONE, true>(g, tile)
-                : launch_tile<A_F32, SPLIT, DOTL_ACT_NONE, false>(g, tile);
+        return out_f16 ? launch_tile<A_F32, SPLIT, DOTL_ACT_GELU, true>(g, tile)
+                       : launch_tile<A_F32, SPLIT, DOTL_ACT_GELU, false>(g, tile);
     }
+    return out_f16 ? launch_tile<A_F32, SPLIT, DOTL_ACT_NONE, true>(g, tile)
+                   : launch_tile<A_F32, SPLIT, DOTL_ACT_NONE, false>(g, tile);
 }
 
-// Tile choice for 256 CUs: the 128x128 tile unless it leaves the grid well
-// short of one workgroup per CU, then 64x64.
-int pick_tile(int64_t M, int64_t N) {
-    const int64_t big = ((M + 127) / 128) * ((N + 127) / 128);
-    return big >= 192 ? 0 : 2;
+// Tile choice for 256 CUs: the largest tile the operand types allow that
+// still gives about one workgroup per CU; below that, the smallest.
+int pick_tile(int64_t M, int64_t N, bool a_f32, bool split) {
+    auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    const int64_t fill = 240;
+    if (!split && !a_f32 && tiles(256, 256) >= fill) return 3;
+    if (!split && tiles(256, 128) >= fill) return 1;
+    if (tiles(128, 128) >= fill) return 0;
+    if (tiles(128, 64) >= fill) return 4;
+    return 2;
 }
 
 }  // namespace
@@ -377,7 +435,8 @@ extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const v
     using namespace dotl;
     clear_error();
     const char* who = act == DOTL_ACT_GELU ? "linear_gelu" : "linear_bias";
-    DOTL_REQUIRE(x_dtype == DOTL_F32 || x_dtype == DOTL_F16, "%s: x must be float32 or float16", who);
+    DOTL_REQUIRE(x_dtype == DOTL_F32 || x_dtype == DOTL_F16 || x_dtype == DOTL_F16X2,
+                 "%s: x must be float32, float16 or split float16", who);
     DOTL_REQUIRE(out_dtype == DOTL_F32 || out_dtype == DOTL_F16, "%s: out must be float32 or float16", who);
     DOTL_REQUIRE(act == DOTL_ACT_NONE || act == DOTL_ACT_GELU, "%s: unknown activation %d", who, act);
     DOTL_REQUIRE(math == DOTL_MATH_FP16 || math == DOTL_MATH_FP16X3, "%s: unknown math %d", who, math);
@@ -386,27 +445,51 @@ extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const v
         set_error(std::string(who) + ": K must be a positive multiple of 8 for 16-byte staging");
         return DOTL_DECLINED;
     }
+    if (x_dtype == DOTL_F16X2 && K % 64 != 0) {
+        set_error(std::string(who) + ": a split-fp16 x needs K % 64 == 0");
+        return DOTL_DECLINED;
+    }
     DOTL_REQUIRE(math != DOTL_MATH_FP16X3 || w_lo != nullptr,
                  "%s: the fp16x3 math needs the split weight residual", who);
     DOTL_REQUIRE(((M + 63) / 64) * ((N + 63) / 64) <= 0x7fffffff, "%s: too large", who);
+    DOTL_REQUIRE(tile == -1 || (tile >= 0 && tile <= 4) || (tile >= 100 && tile <= 104),
+                 "%s: unknown tile id %d", who, tile);
     if (M == 0 || N == 0) return DOTL_OK;
     DOTL_REQUIRE(x && w_hi && bias && out, "%s: null pointer", who);
     const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_hi) |
                             reinterpret_cast<uintptr_t>(w_lo);
     DOTL_REQUIRE(align % 16 == 0, "%s: x and W must be 16-byte aligned", who);
+    const bool of16 = out_dtype == DOTL_F16;
+    const bool split = math == DOTL_MATH_FP16X3;
+
+    // LDS-DMA pipelined kernel: fp16 operands, K a multiple of 64.
+    const bool force_staged = tile >= 100;
+    if (!force_staged && x_dtype != DOTL_F32 && K % 64 == 0) {
+        const _Float16* xh = static_cast<const _Float16*>(x);
+        const _Float16* xl = x_dtype == DOTL_F16X2 ? xh + M * K : nullptr;
+        const int passes = !split ? 1 : (x_dtype == DOTL_F16X2 ? 3 : 2);
+        const int t = tile < 0 ? pick_dma_tile(M, N, passes) : tile;
+        if (launch_gemm_dma(xh, xl, static_cast<const _Float16*>(w_hi),
+                            static_cast<const _Float16*>(w_lo), bias, out, M, N, K, passes, act,
+                            of16, t, as_stream(stream))) {
+            return check_launch(who);
+        }
+        DOTL_REQUIRE(x_dtype != DOTL_F16X2, "%s: tile id %d is not built for three passes", who, tile);
+    }
+    DOTL_REQUIRE(x_dtype != DOTL_F16X2, "%s: split-fp16 x is served by the pipelined kernel only", who);
 
     GemmArgs g{x, static_cast<const _Float16*>(w_hi), static_cast<const _Float16*>(w_lo), bias,
                out, M, N, K, as_stream(stream)};
-    const int t = tile < 0 ? pick_tile(M, N) : tile;
-    DOTL_REQUIRE(t == 0 || t == 2, "%s: unknown tile id %d", who, tile);
-    const bool of16 = out_dtype == DOTL_F16;
-    if (math == DOTL_MATH_FP16X3) {
-        if (x_dtype == DOTL_F32) launch_epilogue<true, true>(g, t, act, of16);
-        else launch_epilogue<false, true>(g, t, act, of16);
-    } else if (x_dtype == DOTL_F32) {
-        launch_epilogue<true, false>(g, t, act, of16);
+    const bool a_f32 = x_dtype == DOTL_F32;
+    const int t = tile < 0 ? pick_tile(M, N, a_f32, split) : (tile % 100);
+    bool ok;
+    if (split) {
+        ok = a_f32 ? launch_epilogue<true, true>(g, t, act, of16)
+                   : launch_epilogue<false, true>(g, t, act, of16);
     } else {
-        launch_epilogue<false, false>(g, t, act, of16);
+        ok = a_f32 ? launch_epilogue<true, false>(g, t, act, of16)
+                   : launch_epilogue<false, false>(g, t, act, of16);
     }
+    DOTL_REQUIRE(ok, "%s: tile id %d is not built for these operand types", who, tile);
     return check_launch(who);
 }

@@ -1,0 +1,476 @@
+// out = act(x @ W^T + bias) on gfx950 MFMA, operands streamed HBM -> LDS by
+// the LDS-DMA loads (global_load_lds_dwordx4), NS pipeline stages deep.
+//
+// The fast path behind dotl_linear for fp16 operands (x fp16, or x as split
+// fp16 hi/lo planes) with K a multiple of 64; gemm.hip's register-staged
+// kernel serves everything else (fp32 x, ragged K).
+//
+// MI355X design:
+//   * no staging registers: each lane's 16-byte load lands directly in LDS
+//     (the wave's 64 lanes fill one contiguous 1 KiB run, lane l at +16 l),
+//     so the pipeline can be 4-8 stages deep (up to 144 KiB of the CU's
+//     160 KiB LDS) without spending VGPRs. Measured on MI355X, a CU's
+//     operand stream is latency-bound: ~1.6 us per 64 KiB batch in flight,
+//     so feeding a 256x256 tile at the MFMA rate takes ~100 KiB in flight.
+//     K tiles are therefore 32 deep (BK = 32: 32 KiB per 256x256 stage) and
+//     the stages many, NS - 1 of them in flight while one is multiplied;
+//   * each stage is its own __shared__ array and the K loop is unrolled by
+//     NS, so every LDS read names a stage the in-flight DMA provably does not
+//     write: the compiler then adds no conservative vmcnt(0) before the reads;
+//     the kernel waits itself, for exactly the loads of the tile it is about
+//     to read (vmcnt = loads of the younger tiles still allowed in flight);
+//   * LDS rows are BK*2 bytes with the 16-byte chunks XOR-swizzled: a
+//     ds_read_b128 serves 16 lanes per pass over the 64 four-byte banks, and
+//     the 16 rows a fragment read touches then sit on 16 distinct 16-byte
+//     bank groups (chunk ^ (row / rows-per-256B) % chunks-per-row),
+//     conflict-free without padding (which would break the DMA's contiguous
+//     lane layout). The swizzle is applied on the global side: each DMA lane
+//     writes a fixed physical chunk and loads the logical chunk that maps
+//     there;
+//   * rows past M (or N) are clamped to the last valid row -- those outputs
+//     are never stored -- so every DMA is in bounds and branch-free; K must
+//     be a multiple of 64 (no K tail);
+//   * PASSES = 1: x*W. 2: x*W + 2^-12 x*lo(W) (x exact in fp16). 3: also
+//     + 2^-12 lo(x)*W, with x given as fp16 hi/lo planes: fp32-class
+//     products on the fp16 matrix cores, in two fp32 accumulators;
+//   * 2 x 2 wavefronts, each a (BM/2) x (BN/2) block of 32x32 accumulators,
+//     issued as W x A^T so every accumulator holds a C^T tile: each lane then
+//     owns runs of 4 consecutive output columns of one row, and the epilogue
+//     (bias from LDS, GELU, narrowing) stores them 16 or 8 bytes at a time
+//     from one row address per tile. The epilogue's cost matters here: with
+//     one workgroup per CU nothing overlaps it, and at the configs' short K
+//     (256-512) it was costing more than the MFMAs.
+#include "dotl_common.h"
+
+namespace dotl {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kXcds = 8;
+constexpr int kGroupM = 8;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void tile_of(int64_t id, int64_t nm, int64_t nn, int64_t& mt,
+                                        int64_t& nt) {
+    const int64_t total = nm * nn;
+    const int64_t per = total / kXcds;
+    if (id < per * kXcds) id = (id % kXcds) * per + id / kXcds;
+    const int64_t in_group = kGroupM * nn;
+    const int64_t group = id / in_group;
+    const int64_t first_m = group * kGroupM;
+    const int64_t gsize = min(static_cast<int64_t>(kGroupM), nm - first_m);
+    const int64_t r = id - group * in_group;
+    mt = first_m + r % gsize;
+    nt = r / gsize;
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier for the pipeline. __syncthreads() carries a release
+// fence, which would make every wave drain ALL its outstanding DMAs
+// (vmcnt(0)) -- including the younger tiles that are meant to stay in
+// flight. Here the wave first waits (explicitly, before calling this) for the
+// DMAs of the tile about to be read, and the barrier only needs this wave's
+// LDS reads of the stage about to be refilled to be complete (lgkmcnt(0)).
+// The memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void stage_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int BM, int BN, int BK, int PASSES>
+struct DmaLayout {
+    // rows of BK halves in one stage: A, W, then lo(W) (PASSES >= 2), lo(A) (PASSES == 3)
+    static constexpr int CPR = BK / 8;               // 16-byte chunks per row
+    static constexpr int ROWS_PER_DMA = 64 / CPR;    // rows one wave instruction fills
+    static constexpr int ROWS_PER_ROUND = 4 * ROWS_PER_DMA;
+    static constexpr int SWZ_DIV = 256 / (BK * 2);   // rows per 256-byte bank sweep
+    static constexpr int A_ROW = 0;
+    static constexpr int W_ROW = BM;
+    static constexpr int WLO_ROW = BM + BN;
+    static constexpr int ALO_ROW = WLO_ROW + (PASSES >= 2 ? BN : 0);
+    static constexpr int ROWS = ALO_ROW + (PASSES == 3 ? BM : 0);
+    static constexpr int HALVES = ROWS * BK;
+    static constexpr int LOADS = ROWS / ROWS_PER_ROUND;   // DMA instructions per wave per stage
+    static_assert(BM % ROWS_PER_ROUND == 0 && BN % ROWS_PER_ROUND == 0, "rows per round");
+    __device__ __forceinline__ static int swz(int row) { return (row / SWZ_DIV) % CPR; }
+};
+
+// One 16-byte-per-lane LDS-DMA load: lane l's 16 bytes at g land at
+// lds + 16 l. Issued from inline assembly so the compiler's wait-count
+// bookkeeping does not see it: the compiler would otherwise drain every
+// outstanding DMA (vmcnt(0)) before any read of a stage that still has one in
+// flight, collapsing the pipeline. The kernel's own wait_vmcnt calls order
+// the reads instead. M0 (the LDS base register of the instruction) is saved
+// and restored around it.
+__device__ __forceinline__ void dma16(const void* g, const _Float16* lds) {
+    const unsigned base = static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_void_t*)(lds)));
+    unsigned saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %2, off\n\t"
+        "s_nop 0\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(base), "v"(g)
+        : "memory");
+}
+
+// Fill `ROWS` rows of a stage region from src (row pitch K halves), rows
+// past `nrows` clamped. One DMA instruction per wave per ROWS_PER_DMA rows.
+template <typename L, int ROWS>
+__device__ __forceinline__ void dma_rows(_Float16* lds_region, const _Float16* __restrict__ src,
+                                         int64_t row0, int64_t nrows, int64_t K, int64_t k0,
+                                         int wave, int lane) {
+    constexpr int BK = L::CPR * 8;
+    const int sub = lane / L::CPR;      // row within this wave's instruction
+    const int pc = lane % L::CPR;       // physical chunk this lane fills
+#pragma unroll
+    for (int i = 0; i < ROWS / L::ROWS_PER_ROUND; ++i) {
+        const int rbase = i * L::ROWS_PER_ROUND + wave * L::ROWS_PER_DMA;
+        const int r = rbase + sub;
+        const int lc = pc ^ L::swz(r);  // logical chunk it holds
+        int64_t gr = row0 + r;
+        gr = gr < nrows ? gr : nrows - 1;
+        const _Float16* g = src + gr * K + k0 + lc * 8;
+        dma16(g, lds_region + rbase * BK);  // wave-uniform destination
+    }
+}
+
+template <int BM, int BN, int BK, int NS, int PASSES, int ACT, bool OUT_F16>
+struct DmaGemm {
+    using L = DmaLayout<BM, BN, BK, PASSES>;
+    static constexpr int WM = BM / 2, WN = BN / 2;
+    static constexpr int TM = WM / 32, TN = WN / 32;
+
+    const _Float16* __restrict__ A;
+    const _Float16* __restrict__ Alo;
+    const _Float16* __restrict__ W;
+    const _Float16* __restrict__ Wlo;
+    int64_t M, N, K, m0, n0, nk;
+    int wave, lane, wm, wn, lr, lg;
+    floatx16 acc[TM][TN];
+    floatx16 acc2[PASSES > 1 ? TM : 1][PASSES > 1 ? TN : 1];
+
+    __device__ __forceinline__ void issue(_Float16* stage, int64_t kt) {
+        const int64_t k0 = kt * BK;
+        dma_rows<L, BM>(stage + L::A_ROW * BK, A, m0, M, K, k0, wave, lane);
+        dma_rows<L, BN>(stage + L::W_ROW * BK, W, n0, N, K, k0, wave, lane);
+        if constexpr (PASSES >= 2) dma_rows<L, BN>(stage + L::WLO_ROW * BK, Wlo, n0, N, K, k0, wave, lane);
+        if constexpr (PASSES == 3) dma_rows<L, BM>(stage + L::ALO_ROW * BK, Alo, m0, M, K, k0, wave, lane);
+    }
+
+    // Fragment of row `row` (tile-local), 16-wide k step `ks`: the 8 halves of
+    // lane group lg, at the swizzled chunk.
+    __device__ __forceinline__ half8 frag(const _Float16* region, int row, int ks) const {
+        const int pc = (ks * 2 + lg) ^ L::swz(row);
+        return *reinterpret_cast<const half8*>(region + row * BK + pc * 8);
+    }
+
+    __device__ __forceinline__ void compute(const _Float16* stage) {
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            half8 a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) a[i] = frag(stage + L::A_ROW * BK, wm * WM + i * 32 + lr, ks);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) b[j] = frag(stage + L::W_ROW * BK, wn * WN + j * 32 + lr, ks);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], a[i], acc[i][j], 0, 0, 0);
+            if constexpr (PASSES >= 2) {
+                half8 bl[TN];
+#pragma unroll
+                for (int j = 0; j < TN; ++j) bl[j] = frag(stage + L::WLO_ROW * BK, wn * WN + j * 32 + lr, ks);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bl[j], a[i], acc2[i][j], 0, 0, 0);
+            }
+            if constexpr (PASSES == 3) {
+                half8 al[TM];
+#pragma unroll
+                for (int i = 0; i < TM; ++i) al[i] = frag(stage + L::ALO_ROW * BK, wm * WM + i * 32 + lr, ks);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], al[i], acc2[i][j], 0, 0, 0);
+            }
+        }
+    }
+
+    // Wait until tile kt's DMAs (this wave's) have landed. Younger tiles
+    // already issued: min(NS - 2, nk - 1 - kt); each is L::LOADS instructions.
+    template <int Y>
+    __device__ __forceinline__ void wait_younger(int64_t younger) const {
+        if constexpr (Y == 0) {
+            wait_vmcnt<0>();
+        } else {
+            if (younger >= Y) { wait_vmcnt<Y * L::LOADS>(); return; }
+            wait_younger<Y - 1>(younger);
+        }
+    }
+    __device__ __forceinline__ void wait_tile(int64_t kt) const {
+        wait_younger<NS - 2>(nk - 1 - kt);
+    }
+};
+
+template <int BM, int BN, int BK, int NS, int PASSES, int ACT, bool OUT_F16>
+__global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
+    const _Float16* __restrict__ A, const _Float16* __restrict__ Alo,
+    const _Float16* __restrict__ W, const _Float16* __restrict__ Wlo,
+    const float* __restrict__ bias, void* __restrict__ C, int64_t M, int64_t N, int64_t K) {
+    using G = DmaGemm<BM, BN, BK, NS, PASSES, ACT, OUT_F16>;
+    using L = typename G::L;
+    static_assert(NS >= 2 && NS <= 8, "2 to 8 stages");
+    static_assert((NS - 2) * L::LOADS < 64, "vmcnt is 6 bits");
+    constexpr int SZ = L::HALVES;
+
+    // One __shared__ array per stage (see the header comment).
+    __shared__ __attribute__((aligned(1024))) _Float16 st0[SZ];
+    __shared__ __attribute__((aligned(1024))) _Float16 st1[SZ];
+    __shared__ __attribute__((aligned(1024))) _Float16 st2[NS > 2 ? SZ : 8];
+    __shared__ __attribute__((aligned(1024))) _Float16 st3[NS > 3 ? SZ : 8];
+    __shared__ __attribute__((aligned(1024))) _Float16 st4[NS > 4 ? SZ : 8];
+    __shared__ __attribute__((aligned(1024))) _Float16 st5[NS > 5 ? SZ : 8];
+    __shared__ __attribute__((aligned(1024))) _Float16 st6[NS > 6 ? SZ : 8];
+    __shared__ __attribute__((aligned(1024))) _Float16 st7[NS > 7 ? SZ : 8];
+
+    G g;
+    g.A = A; g.Alo = Alo; g.W = W; g.Wlo = Wlo;
+    g.M = M; g.N = N; g.K = K;
+    g.lane = threadIdx.x & 63;
+    g.wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    g.wm = g.wave >> 1;
+    g.wn = g.wave & 1;
+    g.lr = g.lane & 31;
+    g.lg = g.lane >> 5;
+    int64_t mt, nt;
+    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, mt, nt);
+    g.m0 = mt * BM;
+    g.n0 = nt * BN;
+    g.nk = K / BK;
+#pragma unroll
+    for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j) {
+            g.acc[i][j] = floatx16{};
+            if constexpr (PASSES > 1) g.acc2[i][j] = floatx16{};
+        }
+
+    auto stage = [&](auto s) -> _Float16* {
+        constexpr int S = decltype(s)::value;
+        if constexpr (S == 0) return st0;
+        else if constexpr (S == 1) return st1;
+        else if constexpr (S == 2) return st2;
+        else if constexpr (S == 3) return st3;
+        else if constexpr (S == 4) return st4;
+        else if constexpr (S == 5) return st5;
+        else if constexpr (S == 6) return st6;
+        else return st7;
+    };
+
+    // The tile's bias columns, staged in LDS before the K loop (the loop's
+    // barriers publish them): read in the epilogue from LDS, they do not wait
+    // behind the epilogue's own global stores the way a global load would.
+    __shared__ __attribute__((aligned(16))) float sbias[BN];
+    for (int c = threadIdx.x; c < BN; c += kThreads) {
+        const int64_t col = g.n0 + c;
+        sbias[c] = col < N ? bias[col] : 0.f;
+    }
+
+    // Prologue: tiles 0 .. NS-2 in flight.
+    auto prologue = [&](auto s) {
+        constexpr int S = decltype(s)::value;
+        if constexpr (S < NS - 1) {
+            if (S < g.nk) g.issue(stage(s), S);
+        }
+    };
+    prologue(std::integral_constant<int, 0>{});
+    prologue(std::integral_constant<int, 1>{});
+    prologue(std::integral_constant<int, 2>{});
+    prologue(std::integral_constant<int, 3>{});
+    prologue(std::integral_constant<int, 4>{});
+    prologue(std::integral_constant<int, 5>{});
+    prologue(std::integral_constant<int, 6>{});
+
+    // One step: wait for tile kt (in stage S), barrier (everyone's DMAs for kt
+    // landed, everyone done reading the stage tile kt + NS - 1 will reuse),
+    // issue tile kt + NS - 1 into stage (S + NS - 1) % NS, multiply tile kt.
+    auto step = [&](auto s, int64_t kt) {
+        constexpr int S = decltype(s)::value;
+        if constexpr (S < NS) {
+            constexpr int NEXT = (S + NS - 1) % NS;
+            g.wait_tile(kt);
+            stage_barrier();
+            if (kt + NS - 1 < g.nk) g.issue(stage(std::integral_constant<int, NEXT>{}), kt + NS - 1);
+            g.compute(stage(s));
+        }
+    };
+
+    int64_t kt = 0;
+    for (; kt + NS <= g.nk; kt += NS) {
+        step(std::integral_constant<int, 0>{}, kt);
+        step(std::integral_constant<int, 1>{}, kt + 1);
+        step(std::integral_constant<int, 2>{}, kt + 2);
+        step(std::integral_constant<int, 3>{}, kt + 3);
+        step(std::integral_constant<int, 4>{}, kt + 4);
+        step(std::integral_constant<int, 5>{}, kt + 5);
+        step(std::integral_constant<int, 6>{}, kt + 6);
+        step(std::integral_constant<int, 7>{}, kt + 7);
+    }
+    // Remainder: fewer than NS tiles, in stages 0, 1, ...
+    if (kt < g.nk) step(std::integral_constant<int, 0>{}, kt);
+    if (kt + 1 < g.nk) step(std::integral_constant<int, 1>{}, kt + 1);
+    if (kt + 2 < g.nk) step(std::integral_constant<int, 2>{}, kt + 2);
+    if (kt + 3 < g.nk) step(std::integral_constant<int, 3>{}, kt + 3);
+    if (kt + 4 < g.nk) step(std::integral_constant<int, 4>{}, kt + 4);
+    if (kt + 5 < g.nk) step(std::integral_constant<int, 5>{}, kt + 5);
+    if (kt + 6 < g.nk) step(std::integral_constant<int, 6>{}, kt + 6);
+
+    // Epilogue. The MFMAs were issued as W x A^T, so each 32x32 accumulator
+    // holds a tile of C^T: lane l owns C row (l % 32) of the tile, and
+    // registers 4g .. 4g+3 hold the four consecutive C columns
+    // 8g + 4 (l / 32) + 0..3 -- one 16-byte (fp32) or 8-byte (fp16) store.
+    const bool vec_ok = (N & 3) == 0;
+#pragma unroll
+    for (int i = 0; i < G::TM; ++i) {
+        const int64_t row = g.m0 + g.wm * G::WM + i * 32 + g.lr;
+        if (row >= M) continue;
+        float* crow32 = static_cast<float*>(C) + row * N;
+        _Float16* crow16 = static_cast<_Float16*>(C) + row * N;
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j) {
+#pragma unroll
+            for (int grp = 0; grp < 4; ++grp) {
+                const int cl = g.wn * G::WN + j * 32 + 8 * grp + 4 * g.lg;  // tile-local column
+                const int64_t col = g.n0 + cl;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float a = g.acc[i][j][4 * grp + e];
+                    if constexpr (PASSES > 1) a += g.acc2[i][j][4 * grp + e] * kLoUnscale;
+                    a += sbias[cl + e];
+                    if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
+                    v[e] = a;
+                }
+                if (vec_ok && col + 4 <= N) {
+                    if constexpr (OUT_F16) {
+                        half4 h;
+                        h[0] = to_half(v[0]); h[1] = to_half(v[1]);
+                        h[2] = to_half(v[2]); h[3] = to_half(v[3]);
+                        *reinterpret_cast<half4*>(crow16 + col) = h;
+                    } else {
+                        *reinterpret_cast<float4*>(crow32 + col) = make_float4(v[0], v[1], v[2], v[3]);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (col + e < N) {
+                            if constexpr (OUT_F16) crow16[col + e] = to_half(v[e]);
+                            else crow32[col + e] = v[e];
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+struct DmaArgs {
+    const _Float16* A;
+    const _Float16* Alo;
+    const _Float16* W;
+    const _Float16* Wlo;
+    const float* bias;
+    void* C;
+    int64_t M, N, K;
+    hipStream_t stream;
+};
+
+template <int BM, int BN, int BK, int NS, int PASSES, int ACT, bool OUT_F16>
+void launch_dma(const DmaArgs& a) {
+    const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, PASSES, ACT, OUT_F16>),
+                       dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, a.stream, a.A,
+                       a.Alo, a.W, a.Wlo, a.bias, a.C, a.M, a.N, a.K);
+}
+
+// Tile ids (dotl_linear's `tile`): 0 128x128, 1 256x128, 2 64x64, 3 256x256,
+// 4 128x64. K tiles of 32; stage counts fill <= 144 KiB of LDS.
+template <int PASSES, int ACT, bool OUT_F16>
+bool dispatch_tile(const DmaArgs& a, int tile) {
+    switch (tile) {
+        case 0:   // stage: 256 / 384 / 512 rows x 64 B = 16 / 24 / 32 KiB
+            if constexpr (PASSES == 1) launch_dma<128, 128, 32, 8, PASSES, ACT, OUT_F16>(a);
+            else if constexpr (PASSES == 2) launch_dma<128, 128, 32, 6, PASSES, ACT, OUT_F16>(a);
+            else launch_dma<128, 128, 32, 4, PASSES, ACT, OUT_F16>(a);
+            return true;
+        case 1:   // 384 rows: 24 KiB
+            if constexpr (PASSES == 1) { launch_dma<256, 128, 32, 6, PASSES, ACT, OUT_F16>(a); return true; }
+            return false;
+        case 2:   // 128 / 192 / 256 rows
+            if constexpr (PASSES == 1) launch_dma<64, 64, 32, 8, PASSES, ACT, OUT_F16>(a);
+            else launch_dma<64, 64, 32, 8, PASSES, ACT, OUT_F16>(a);
+            return true;
+        case 3:   // 512 rows: 32 KiB
+            if constexpr (PASSES == 1) { launch_dma<256, 256, 32, 4, PASSES, ACT, OUT_F16>(a); return true; }
+            return false;
+        case 4:   // 192 / 320 / 384 rows
+            if constexpr (PASSES == 1) launch_dma<128, 64, 32, 8, PASSES, ACT, OUT_F16>(a);
+            else if constexpr (PASSES == 2) launch_dma<128, 64, 32, 7, PASSES, ACT, OUT_F16>(a);
+            else launch_dma<128, 64, 32, 6, PASSES, ACT, OUT_F16>(a);
+            return true;
+    }
+    return false;
+}
+
+}  // namespace
+
+// Largest tile allowed for this arithmetic that still gives about one
+// workgroup per CU (256 CUs); else the one with the most workgroups.
+int pick_dma_tile(int64_t M, int64_t N, int passes) {
+    auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    const int64_t fill = 240;
+    if (passes == 1 && tiles(256, 256) >= fill) return 3;
+    if (passes == 1 && tiles(256, 128) >= fill) return 1;
+    if (tiles(128, 128) >= fill) return 0;
+    if (tiles(128, 64) >= fill) return 4;
+    return 2;
+}
+
+bool launch_gemm_dma(const _Float16* A, const _Float16* Alo, const _Float16* W,
+                     const _Float16* Wlo, const float* bias, void* C, int64_t M, int64_t N,
+                     int64_t K, int passes, int act, bool out_f16, int tile, hipStream_t stream) {
+    const DmaArgs a{A, Alo, W, Wlo, bias, C, M, N, K, stream};
+    auto by_out = [&](auto p) {
+        constexpr int P = decltype(p)::value;
+        if (act == DOTL_ACT_GELU) {
+            return out_f16 ? dispatch_tile<P, DOTL_ACT_GELU, true>(a, tile)
+                           : dispatch_tile<P, DOTL_ACT_GELU, false>(a, tile);
+        }
+        return out_f16 ? dispatch_tile<P, DOTL_ACT_NONE, true>(a, tile)
+                       : dispatch_tile<P, DOTL_ACT_NONE, false>(a, tile);
+    };
+    switch (passes) {
+        case 1: return by_out(std::integral_constant<int, 1>{});
+        case 2: return by_out(std::integral_constant<int, 2>{});
+        case 3: return by_out(std::integral_constant<int, 3>{});
+    }
+    return false;
+}
+
+}  // namespace dotl

@@ -3,7 +3,8 @@
 // Replaces fused_add_layernorm / fused_layernorm (reference
 // csrc/add_layernorm.cuh:491-692). Same contract: x_new = x + sub, normed =
 // (x_new - mean) * rsqrt(var + eps) * w + b with the biased variance, fp32
-// statistics, the normed output optionally narrowed to fp16 with RNE.
+// statistics, the normed output optionally narrowed to fp16 with RNE, or
+// split into fp16 hi/lo planes for the fp16x3 GEMM that consumes it.
 //
 // Layout and mapping (MI355X):
 //   * one 64-lane wavefront per row, the whole row held in registers, so the
@@ -41,7 +42,7 @@ __device__ __forceinline__ float4 load_sum4(const float* __restrict__ x,
 
 // Vector path: D % 4 == 0 and D <= 256 * CH. Chunk c of lane l covers row
 // elements [4 * (c * 64 + l), +4).
-template <int CH, bool HAS_SUB, bool WRITE_XNEW, bool NORMED_F16>
+template <int CH, bool HAS_SUB, bool WRITE_XNEW, int NORMED>
 __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     const float* __restrict__ x, const float* __restrict__ sub,
     const float* __restrict__ w, const float* __restrict__ b,
@@ -106,11 +107,17 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
                 o.y = ((v[c].y - mean_est) - delta) * rstd * ww.y + bb.y;
                 o.z = ((v[c].z - mean_est) - delta) * rstd * ww.z + bb.z;
                 o.w = ((v[c].w - mean_est) - delta) * rstd * ww.w + bb.w;
-                if constexpr (NORMED_F16) {
+                if constexpr (NORMED == DOTL_F16 || NORMED == DOTL_F16X2) {
                     half4 h;
                     h[0] = to_half(o.x); h[1] = to_half(o.y);
                     h[2] = to_half(o.z); h[3] = to_half(o.w);
                     *reinterpret_cast<half4*>(static_cast<_Float16*>(normed) + base + col) = h;
+                    if constexpr (NORMED == DOTL_F16X2) {
+                        half4 l;
+                        l[0] = split_lo(o.x, h[0]); l[1] = split_lo(o.y, h[1]);
+                        l[2] = split_lo(o.z, h[2]); l[3] = split_lo(o.w, h[3]);
+                        *reinterpret_cast<half4*>(static_cast<_Float16*>(normed) + rows * D + base + col) = l;
+                    }
                 } else {
                     *reinterpret_cast<float4*>(static_cast<float*>(normed) + base + col) = o;
                 }
@@ -121,7 +128,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
 
 // Scalar path for any D in [1, 64 * EPL]: element e of lane l is column
 // e * 64 + l. Used when D % 4 != 0 (the vector path's 16-byte accesses need it).
-template <int EPL, bool HAS_SUB, bool WRITE_XNEW, bool NORMED_F16>
+template <int EPL, bool HAS_SUB, bool WRITE_XNEW, int NORMED>
 __global__ __launch_bounds__(256) void layernorm_scalar_kernel(
     const float* __restrict__ x, const float* __restrict__ sub,
     const float* __restrict__ w, const float* __restrict__ b,
@@ -171,8 +178,11 @@ __global__ __launch_bounds__(256) void layernorm_scalar_kernel(
             if (col < D) {
                 if constexpr (WRITE_XNEW) x_new[base + col] = v[e];
                 const float o = ((v[e] - mean_est) - delta) * rstd * w[col] + b[col];
-                if constexpr (NORMED_F16) {
-                    static_cast<_Float16*>(normed)[base + col] = to_half(o);
+                if constexpr (NORMED == DOTL_F16 || NORMED == DOTL_F16X2) {
+                    const _Float16 h = to_half(o);
+                    static_cast<_Float16*>(normed)[base + col] = h;
+                    if constexpr (NORMED == DOTL_F16X2)
+                        static_cast<_Float16*>(normed)[rows * D + base + col] = split_lo(o, h);
                 } else {
                     static_cast<float*>(normed)[base + col] = o;
                 }
@@ -202,21 +212,21 @@ unsigned grid_for(int64_t rows) {
     return static_cast<unsigned>(want < cap ? (want > 0 ? want : 1) : cap);
 }
 
-template <int CH, bool HAS_SUB, bool WX, bool F16>
+template <int CH, bool HAS_SUB, bool WX, int F16>
 void launch_vec(const LnArgs& a) {
     hipLaunchKernelGGL((layernorm_vec_kernel<CH, HAS_SUB, WX, F16>), dim3(grid_for(a.rows)),
                        dim3(256), 0, a.stream, a.x, a.sub, a.w, a.b, a.x_new, a.normed,
                        a.rows, a.D, a.eps);
 }
 
-template <int EPL, bool HAS_SUB, bool WX, bool F16>
+template <int EPL, bool HAS_SUB, bool WX, int F16>
 void launch_scalar(const LnArgs& a) {
     hipLaunchKernelGGL((layernorm_scalar_kernel<EPL, HAS_SUB, WX, F16>), dim3(grid_for(a.rows)),
                        dim3(256), 0, a.stream, a.x, a.sub, a.w, a.b, a.x_new, a.normed,
                        a.rows, a.D, a.eps);
 }
 
-template <bool HAS_SUB, bool WX, bool F16>
+template <bool HAS_SUB, bool WX, int F16>
 void dispatch_width(const LnArgs& a, bool vec) {
     const int D = a.D;
     if (vec) {
@@ -249,8 +259,8 @@ extern "C" int dotl_layernorm(const void* x, const void* sub, const float* weigh
         set_error(std::string(who) + ": this build serves float32 tensors only");
         return DOTL_DECLINED;
     }
-    DOTL_REQUIRE(normed_dtype == DOTL_F32 || normed_dtype == DOTL_F16,
-                 "%s: normed dtype must be float32 or float16", who);
+    DOTL_REQUIRE(normed_dtype == DOTL_F32 || normed_dtype == DOTL_F16 || normed_dtype == DOTL_F16X2,
+                 "%s: normed dtype must be float32, float16 or split float16", who);
     DOTL_REQUIRE(D >= 1 && D <= 8192, "%s: last dimension %lld outside [1, 8192]", who,
                  static_cast<long long>(D));
     DOTL_REQUIRE(rows >= 0, "%s: negative row count", who);
@@ -268,15 +278,20 @@ extern "C" int dotl_layernorm(const void* x, const void* sub, const float* weigh
     LnArgs a{static_cast<const float*>(x), static_cast<const float*>(sub), weight, bias,
              static_cast<float*>(x_new), normed, rows, static_cast<int>(D),
              static_cast<float>(eps), as_stream(stream)};
-    const bool f16 = normed_dtype == DOTL_F16;
-    if (sub) {
-        if (x_new) {
-            f16 ? dispatch_width<true, true, true>(a, vec) : dispatch_width<true, true, false>(a, vec);
-        } else {
-            f16 ? dispatch_width<true, false, true>(a, vec) : dispatch_width<true, false, false>(a, vec);
+    auto by_out = [&](auto has_sub, auto wx) {
+        constexpr bool HS = decltype(has_sub)::value;
+        constexpr bool WX = decltype(wx)::value;
+        switch (normed_dtype) {
+            case DOTL_F16: dispatch_width<HS, WX, DOTL_F16>(a, vec); break;
+            case DOTL_F16X2: dispatch_width<HS, WX, DOTL_F16X2>(a, vec); break;
+            default: dispatch_width<HS, WX, DOTL_F32>(a, vec); break;
         }
+    };
+    if (sub) {
+        if (x_new) by_out(std::true_type{}, std::true_type{});
+        else by_out(std::true_type{}, std::false_type{});
     } else {
-        f16 ? dispatch_width<false, false, true>(a, vec) : dispatch_width<false, false, false>(a, vec);
+        by_out(std::false_type{}, std::false_type{});
     }
     return check_launch(who);
 }

@@ -43,6 +43,7 @@ DOTL_OK = 0
 DOTL_DECLINED = 1
 DOTL_F32 = 0
 DOTL_F16 = 1
+DOTL_F16X2 = 2
 DOTL_ACT_NONE = 0
 DOTL_ACT_GELU = 1
 DOTL_MATH_FP16 = 0
@@ -53,7 +54,7 @@ EXPORTED_SYMBOLS = (
     "dotl_last_error", "dotl_abi_version", "dotl_target", "dotl_smoke_test_identity",
     "dotl_mfma_layout_probe", "dotl_layernorm", "dotl_weight_split", "dotl_linear",
     "dotl_attention_forward", "dotl_ffn_block", "dotl_wmma_set_fp16", "dotl_wmma_fp16",
-    "dotl_wmma_set_cp_async", "dotl_wmma_cp_async_mode",
+    "dotl_wmma_set_cp_async", "dotl_wmma_cp_async_mode", "dotl_lds_dma_probe",
 )
 
 _kernels = None
@@ -93,6 +94,8 @@ def _declare(lib) -> None:
     lib.dotl_smoke_test_identity.argtypes = [vp, vp, i64, vp]
     lib.dotl_mfma_layout_probe.restype = i32
     lib.dotl_mfma_layout_probe.argtypes = [vp, vp]
+    lib.dotl_lds_dma_probe.restype = i32
+    lib.dotl_lds_dma_probe.argtypes = [vp, vp, vp]
     lib.dotl_layernorm.restype = i32
     lib.dotl_layernorm.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, c.c_double, i32, i32, vp]
     lib.dotl_weight_split.restype = i32
@@ -203,9 +206,19 @@ class Kernels:
         self._check(self._lib.dotl_mfma_layout_probe(out.data_ptr(), self._stream(out.device)))
         return out
 
+    def lds_dma_probe(self, src):
+        """LDS contents after one wave's 16-byte-per-lane LDS-DMA load of src (256 int32)."""
+        import torch
+
+        out = torch.empty(512, dtype=torch.int32, device=src.device)
+        self._check(self._lib.dotl_lds_dma_probe(src.data_ptr(), out.data_ptr(),
+                                                 self._stream(src.device)))
+        return out
+
     # -- LayerNorm (reference csrc/add_layernorm.cuh:491-692) -----------------------
 
-    def _layernorm(self, who, x, sub, weight, bias, eps, normed_half, write_xnew=True):
+    def _layernorm(self, who, x, sub, weight, bias, eps, normed_half, write_xnew=True,
+                   split=False):
         import torch
 
         self._require_cuda(who, x, sub, weight, bias)
@@ -230,14 +243,18 @@ class Kernels:
         sc = sub.contiguous() if sub is not None else None
         wc, bc = weight.contiguous(), bias.contiguous()
         x_new = torch.empty_like(xc) if (sc is not None and write_xnew) else None
-        normed = torch.empty(xc.shape, dtype=torch.float16 if normed_half else torch.float32,
-                             device=xc.device)
+        if split:
+            normed = torch.empty((2, *xc.shape), dtype=torch.float16, device=xc.device)
+            ncode = DOTL_F16X2
+        else:
+            normed = torch.empty(xc.shape, dtype=torch.float16 if normed_half else torch.float32,
+                                 device=xc.device)
+            ncode = DOTL_F16 if normed_half else DOTL_F32
         rows = xc.numel() // D if D else 0
         rc = self._lib.dotl_layernorm(
             xc.data_ptr(), sc.data_ptr() if sc is not None else None, wc.data_ptr(),
             bc.data_ptr(), x_new.data_ptr() if x_new is not None else None, normed.data_ptr(),
-            rows, D, float(eps), DOTL_F32, DOTL_F16 if normed_half else DOTL_F32,
-            self._stream(x.device))
+            rows, D, float(eps), DOTL_F32, ncode, self._stream(x.device))
         self._check(rc)
         if rc == DOTL_DECLINED:
             raise RuntimeError(self._err())
@@ -265,6 +282,22 @@ class Kernels:
         """Plain LayerNorm over the last dimension."""
         _, normed = self._layernorm("fused_layernorm", x, None, weight, bias, eps, out_half)
         return normed
+
+    def fused_layernorm_split(self, x, weight, bias, eps=1e-5):
+        """LayerNorm as split fp16 planes [2, *x.shape]: hi, then lo = (v - hi) * 2^12.
+
+        Not in the reference's surface: the input form of linear_bias_split,
+        the fp32-class (fp16x3) projection. Same bytes as an fp32 output.
+        """
+        _, planes = self._layernorm("fused_layernorm", x, None, weight, bias, eps, False,
+                                    split=True)
+        return planes
+
+    def fused_add_layernorm_split(self, x, sub, weight, bias, eps=1e-5):
+        """[x + sub, LayerNorm(x + sub) as split fp16 planes]."""
+        x_new, planes = self._layernorm("fused_add_layernorm", x, sub, weight, bias, eps, False,
+                                        split=True)
+        return [x_new, planes]
 
     # -- GEMM (reference csrc/linear_gelu.cuh:598-756) -------------------------------
 
@@ -328,6 +361,34 @@ class Kernels:
             xc.data_ptr(), xcode, hi.data_ptr(), lo.data_ptr() if lo is not None else None,
             bc.data_ptr(), out.data_ptr(), DOTL_F16 if out_half else DOTL_F32, M, N, K, act, m,
             int(tile), self._stream(x.device)))
+        if rc == DOTL_DECLINED:
+            return None
+        return out
+
+    def linear_bias_split(self, planes, weight, bias, tile=-1, out_half=False):
+        """x @ weight^T + bias with x given as split fp16 planes [2, ..., K]
+        (fused_layernorm_split's output), in the fp16x3 arithmetic: three MFMA
+        passes, fp32-class products. Not in the reference's surface.
+        """
+        import torch
+
+        who = "linear_bias"
+        self._require_cuda(who, planes, weight, bias)
+        if planes.dtype != torch.float16 or planes.dim() < 2 or planes.shape[0] != 2:
+            raise RuntimeError(f"{who}: split input must be float16 [2, ..., K]")
+        if planes.shape[-1] != weight.shape[1] or bias.numel() != weight.shape[0]:
+            raise RuntimeError(f"{who}: shapes disagree: {tuple(planes.shape)}, "
+                               f"{tuple(weight.shape)}, {tuple(bias.shape)}")
+        K, N = weight.shape[1], weight.shape[0]
+        pc = planes.contiguous()
+        M = pc[0].numel() // K
+        hi, lo = self.weight_half(weight, True)
+        out = torch.empty((*pc.shape[1:-1], N), dtype=torch.float16 if out_half else torch.float32,
+                          device=pc.device)
+        rc = self._check(self._lib.dotl_linear(
+            pc.data_ptr(), DOTL_F16X2, hi.data_ptr(), lo.data_ptr(), bias.contiguous().data_ptr(),
+            out.data_ptr(), DOTL_F16 if out_half else DOTL_F32, M, N, K, DOTL_ACT_NONE,
+            DOTL_MATH_FP16X3, int(tile), self._stream(pc.device)))
         if rc == DOTL_DECLINED:
             return None
         return out

@@ -84,6 +84,58 @@ def _linear_gelu(x: torch.Tensor, lin, out_half: bool = False) -> torch.Tensor:
     return out.half() if out_half else out
 
 
+def _split_planes(t: torch.Tensor) -> torch.Tensor:
+    """fp32 -> [2, ...] fp16 planes: hi = fp16(t), lo = fp16((t - hi) * 2^12)."""
+    hi = t.half()
+    lo = ((t - hi.float()) * 4096.0).half()
+    return torch.stack([hi, lo])
+
+
+def _normed_split_wanted() -> bool:
+    """Should a LayerNorm feeding the QKV projection emit split fp16 planes?
+
+    Yes exactly when that projection runs the fp16x3 arithmetic on the
+    pipelined GEMM: the planes carry ~22 bits of the LayerNorm output in the
+    same bytes as fp32, already in the form the three MFMA passes read.
+    """
+    return (config.LINEAR_BIAS == "auto" and config.QKV_PRECISION == "fp16x3"
+            and config.NORMED_FP16 != "off")
+
+
+def _layernorm_split(x: torch.Tensor, norm) -> torch.Tensor:
+    """LayerNorm(x) as split fp16 planes [2, *x.shape]."""
+    kernels = _custom_kernels()
+    if kernels is not None:
+        return kernels.fused_layernorm_split(x, norm.weight, norm.bias, norm.eps)
+    fallback_counts["layernorm"] += 1
+    return _split_planes(F.layer_norm(x, (x.shape[-1],), norm.weight, norm.bias, norm.eps))
+
+
+def _add_layernorm_split(x: torch.Tensor, sub: torch.Tensor, norm):
+    """(x + sub, LayerNorm(x + sub) as split fp16 planes)."""
+    kernels = _custom_kernels()
+    if kernels is not None:
+        return tuple(kernels.fused_add_layernorm_split(x, sub, norm.weight, norm.bias, norm.eps))
+    fallback_counts["add_layernorm"] += 1
+    total = x + sub
+    return total, _split_planes(F.layer_norm(total, (total.shape[-1],), norm.weight,
+                                             norm.bias, norm.eps))
+
+
+def _linear_bias_split(planes: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
+                       out_half: bool = False) -> torch.Tensor:
+    """planes-as-x @ weight^T + bias in the fp16x3 arithmetic."""
+    kernels = _custom_kernels()
+    if kernels is not None:
+        out = kernels.linear_bias_split(planes, weight, bias, -1, out_half)
+        if out is not None:
+            return out
+    fallback_counts["linear_bias"] += 1
+    x = planes[0].float() + planes[1].float() / 4096.0
+    out = F.linear(x, weight, bias)
+    return out.half() if out_half else out
+
+
 def _layernorm(x: torch.Tensor, norm, out_half: bool = False) -> torch.Tensor:
     """LayerNorm(x) * w + b: the model's one norm with no residual before it."""
     if config.LAYERNORM != "off":

@@ -13,9 +13,11 @@ import torch
 import torch.nn as nn
 
 from . import config
-from .kernels import (_add_layernorm, _attention_dispatch, _attention_wants_fp16, _ffn_block,
-                      _gelu_input_wants_fp16, _gelu_output_wants_fp16, _layernorm,
-                      _linear_bias, _linear_gelu, _normed_wants_fp16, _qkv_math_code)
+from .kernels import (_add_layernorm, _add_layernorm_split, _attention_dispatch,
+                      _attention_wants_fp16, _ffn_block, _gelu_input_wants_fp16,
+                      _gelu_output_wants_fp16, _layernorm, _layernorm_split, _linear_bias,
+                      _linear_bias_split, _linear_gelu, _normed_split_wanted,
+                      _normed_wants_fp16, _qkv_math_code)
 from .util import _version_or_none
 
 
@@ -45,7 +47,10 @@ class MyLayerNorm(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         # Reached by the model's first norm (every other one is fused into a
         # residual add) and by the padded path's trailing norm. Its consumer
-        # is a QKV projection, so it may narrow on the same terms.
+        # is a QKV projection: split fp16 planes for the fp16x3 projection, or
+        # fp16 where that projection narrows anyway.
+        if _normed_split_wanted():
+            return _layernorm_split(x, self)
         rows = x.numel() // x.shape[-1]
         return _layernorm(x, self, out_half=_normed_wants_fp16(rows, x.shape[-1]))
 
@@ -90,14 +95,20 @@ class MySelfAttention(nn.Module):
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,
                 causal: bool = False, mask_is_trivial: bool = False) -> torch.Tensor:
-        batch, seq_len, _ = x.shape
+        """`x` is [B, S, D], or [2, B, S, D] split fp16 planes of it (the form
+        a LayerNorm emits for the fp16x3 projection)."""
+        split = x.dim() == 4
+        batch, seq_len = (x.shape[1], x.shape[2]) if split else (x.shape[0], x.shape[1])
         qkv_w, qkv_b = self._get_qkv_weight()
         rows = batch * seq_len
         # fp16 q/k/v when attention contracts in fp16: the projection's
         # epilogue applies the RNE attention would apply while staging.
         want_half = (_attention_wants_fp16()
                      and config._QKV_FP16_MIN_ROWS <= rows <= config._LINEAR_BIAS_MAX_ROWS)
-        qkv = _linear_bias(x, qkv_w, qkv_b, out_half=want_half, math=_qkv_math_code())
+        if split:
+            qkv = _linear_bias_split(x, qkv_w, qkv_b, out_half=want_half)
+        else:
+            qkv = _linear_bias(x, qkv_w, qkv_b, out_half=want_half, math=_qkv_math_code())
         # [B, S, 3, H, hd] -> three strided [B, H, S, hd] views; no copies.
         q, k, v = (qkv.view(batch, seq_len, 3, self.num_heads, self.head_dim)
                    .permute(2, 0, 3, 1, 4).unbind(0))
@@ -153,6 +164,8 @@ class MyTransformerBlock(nn.Module):
             x = (x + ffn_out).masked_fill(~valid_token_mask[..., None], 0)
             return x, next_norm(x) if not next_norm_is_output else _final_norm(x, next_norm)
 
+        if not next_norm_is_output and _normed_split_wanted():
+            return _add_layernorm_split(x, ffn_out, next_norm)
         trailing_half = (not next_norm_is_output
                          and _normed_wants_fp16(rows, x.shape[-1]))
         return _add_layernorm(x, ffn_out, next_norm, normed_half=trailing_half)

@@ -46,6 +46,8 @@ extern "C" {
 /* dtype codes */
 #define DOTL_F32 0
 #define DOTL_F16 1
+#define DOTL_F16X2 2 /* split fp16 planes [2][n]: hi = fp16(v), then
+                        lo = fp16((v - hi) * 2^12); v ~= hi + lo * 2^-12 */
 
 /* linear activation codes */
 #define DOTL_ACT_NONE 0
@@ -87,8 +89,9 @@ int dotl_mfma_layout_probe(int32_t* out, void* stream);
  *   weight,bias [D] float32
  *   x_new       [rows, D] float32 output, x + sub (rounded to fp32); may be
  *               NULL to skip the store (required NULL when sub == NULL)
- *   normed      [rows, D] output of dtype normed_dtype (DOTL_F32 or DOTL_F16,
- *               RNE narrowing), LayerNorm(x + sub) * weight + bias
+ *   normed      [rows, D] output of dtype normed_dtype (DOTL_F32; DOTL_F16, RNE
+ *               narrowing; or DOTL_F16X2, [2][rows][D] split planes for the
+ *               DOTL_MATH_FP16X3 GEMM), LayerNorm(x + sub) * weight + bias
  *   Statistics: fp32, mean then the centred sum of squares (biased variance),
  *   eps inside the square root.
  *   D in [1, 8192]; rows >= 0.
@@ -112,16 +115,21 @@ int dotl_weight_split(const float* w, void* w_hi, void* w_lo, int64_t n, void* s
  * Replaces linear_bias / linear_gelu (reference csrc/linear_gelu.cuh:598-756).
  *
  *   x         [M, K] contiguous, x_dtype DOTL_F32 (narrowed with RNE when
- *             staged) or DOTL_F16
+ *             staged), DOTL_F16, or DOTL_F16X2 ([2][M][K] hi/lo planes)
  *   w_hi      [N, K] fp16 from dotl_weight_split
  *   w_lo      [N, K] fp16 scaled residual; required for DOTL_MATH_FP16X3
  *   bias      [N] float32 (required; the reference's kernels always add one)
  *   out       [M, N], out_dtype DOTL_F32 or DOTL_F16 (RNE)
  *   act       DOTL_ACT_NONE / DOTL_ACT_GELU, applied in fp32 before the store
  *   math      DOTL_MATH_FP16 or DOTL_MATH_FP16X3 (an fp16 x is exact in
- *             fp16, so with it the split path runs two passes: x*hi + x*lo)
- *   tile      -1 auto; otherwise a tile id (0: 128x128, 1: 256x128, 2: 64x64)
- *   Declines when K % 8 != 0.
+ *             fp16, so with it the split path runs two passes: x*hi + x*lo;
+ *             a DOTL_F16X2 x runs three: + lo(x)*hi(W))
+ *   tile      -1 auto; otherwise a tile id (0: 128x128, 1: 256x128 [one
+ *             pass], 2: 64x64, 3: 256x256 [one pass], 4: 128x64); 100 + id
+ *             forces the register-staged kernel (for measurement)
+ *   fp16 / split-fp16 x with K % 64 == 0 runs the LDS-DMA pipelined kernel;
+ *   anything else the register-staged one. Declines when K % 8 != 0, or a
+ *   DOTL_F16X2 x with K % 64 != 0.
  */
 int dotl_linear(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
                 const float* bias, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
@@ -168,6 +176,12 @@ int dotl_ffn_block(const float* x, const float* attn_out, const float* norm1_w,
                    const float* ffn_out_w, const float* ffn_out_b, const float* norm2_w,
                    const float* norm2_b, float* x_out, float* normed_out, int64_t rows,
                    int64_t D, int64_t F, double eps, void* stream);
+
+/* Writes where each lane's 16 bytes of one global_load_lds_dwordx4 land in
+ * LDS: src is 256 int32 (64 lanes x 4), out 512 int32 (a zeroed 2 KiB LDS
+ * region after the load, read back). Expected: lane l at bytes [16 l, 16 l + 16).
+ * A test, not a start-up step. */
+int dotl_lds_dma_probe(const int32_t* src, int32_t* out, void* stream);
 
 /* Process-wide knobs with the reference's names
  * (reference csrc/fused_attention.cu:234-339). wmma_set_fp16 selects the

@@ -332,3 +332,87 @@ def test_attention_refusals(kernels):
     with pytest.raises(RuntimeError):
         qb = q.bfloat16()
         kernels.fused_attention_forward(qb, qb, qb, None, False, 0.125, 0, 1, 0)
+
+
+# ---- LDS-DMA pipelined GEMM --------------------------------------------------------
+
+def test_lds_dma_probe(kernels):
+    """One global_load_lds_dwordx4: lane l's 16 bytes land at LDS offset 16 l."""
+    src = torch.arange(256, dtype=torch.int32, device=DEV) * 7 + 3
+    out = kernels.lds_dma_probe(src).cpu().numpy()
+    np.testing.assert_array_equal(out[:256], src.cpu().numpy())
+    assert np.all(out[256:] == 0)
+
+
+@pytest.mark.parametrize("rows,D", [(300, 256), (64, 512), (5, 1024)])
+def test_layernorm_split_planes(kernels, rows, D):
+    r = np.random.default_rng(rows + D)
+    x = r.standard_normal((rows, D)).astype(np.float32)
+    w = (1 + 0.3 * r.standard_normal(D)).astype(np.float32)
+    b = (0.2 * r.standard_normal(D)).astype(np.float32)
+    planes = kernels.fused_layernorm_split(_t(x), _t(w), _t(b), 1e-5)
+    assert planes.dtype == torch.float16 and tuple(planes.shape) == (2, rows, D)
+    hi, lo = planes[0].float().cpu().numpy(), planes[1].float().cpu().numpy()
+    want = torch.nn.functional.layer_norm(torch.from_numpy(x).double(), (D,),
+                                          torch.from_numpy(w).double(),
+                                          torch.from_numpy(b).double(), 1e-5).numpy()
+    # hi is the fp16 rounding, hi + lo * 2^-12 the ~22-bit value
+    assert np.all(np.abs(hi - want) <= np.spacing(np.abs(want).astype(np.float16)).astype(np.float64))
+    np.testing.assert_allclose(hi + lo / 4096.0, want, atol=3e-6, rtol=1e-6)
+    xn, planes2 = kernels.fused_add_layernorm_split(_t(x), _t(x), _t(w), _t(b), 1e-5)
+    assert torch.equal(xn, _t(x) + _t(x))
+
+
+DMA_SHAPES = [(300, 200, 128), (1000, 1024, 256), (64, 2048, 512), (513, 384, 64)]
+
+
+@pytest.mark.parametrize("M,N,K", DMA_SHAPES)
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 4])
+def test_gemm_dma_one_pass(kernels, M, N, K, tile):
+    """fp16 x on the pipelined kernel: every tile, with M and N tails."""
+    x, w, b = _gemm_case(M, N, K, 7 * M + N)
+    want = _h(x) @ _h(w).T + b
+    got = kernels.linear_bias(_t(x).half(), _t(w), _t(b), tile, -1).cpu().numpy()
+    np.testing.assert_allclose(got, want, atol=2e-5 * np.sqrt(K / 128), rtol=1e-5)
+    # the register-staged kernel (tile 100 + id) gives the same numbers
+    staged = kernels.linear_bias(_t(x).half(), _t(w), _t(b), 100 + max(tile, 0), -1)
+    np.testing.assert_allclose(got, staged.cpu().numpy(), atol=2e-5 * np.sqrt(K / 128))
+
+
+@pytest.mark.parametrize("M,N,K", DMA_SHAPES)
+@pytest.mark.parametrize("tile", [-1, 0, 2, 4])
+def test_gemm_dma_split_weight(kernels, M, N, K, tile):
+    """fp16 x with the fp16x3 math: two passes, x * (hi + 2^-12 lo) of the fp32 W."""
+    x, w, b = _gemm_case(M, N, K, 5 * M + N)
+    want = _h(x) @ w.astype(np.float64).T + b
+    got = kernels.linear_bias(_t(x).half(), _t(w), _t(b), tile, 0).cpu().numpy()
+    np.testing.assert_allclose(got, want, atol=3e-6 * np.sqrt(K / 128), rtol=2e-6)
+
+
+@pytest.mark.parametrize("M,N,K", DMA_SHAPES)
+@pytest.mark.parametrize("tile", [-1, 0, 2, 4])
+@pytest.mark.parametrize("act", ["none", "half_out"])
+def test_gemm_dma_split_planes(kernels, M, N, K, tile, act):
+    """Split-plane x: three passes, fp32-class products against the fp64 GEMM."""
+    x, w, b = _gemm_case(M, N, K, 3 * M + N)
+    xt = _t(x)
+    hi = xt.half()
+    lo = ((xt - hi.float()) * 4096.0).half()
+    planes = torch.stack([hi, lo])
+    xr = hi.double().cpu().numpy() + lo.double().cpu().numpy() / 4096.0
+    want = xr @ w.astype(np.float64).T + b
+    got = kernels.linear_bias_split(planes, _t(w), _t(b), tile, act == "half_out")
+    if act == "half_out":
+        want16 = want.astype(np.float16).astype(np.float64)
+        # one fp16 ulp, or the fp32 accumulation's absolute error where the
+        # result is small enough for that to exceed an ulp (cancellation)
+        ulp = np.maximum(np.spacing(np.abs(want16).astype(np.float16)).astype(np.float64),
+                         3e-6 * np.sqrt(K / 128))
+        g = got.double().cpu().numpy()
+        bad = np.abs(g - want16) > ulp
+        if bad.any():
+            i = np.unravel_index(np.argmax(np.abs(g - want16) - ulp), g.shape)
+            raise AssertionError(f"{int(bad.sum())} elements off by more than 1 ulp; worst at {i}: "
+                                 f"got {g[i]!r} want {want[i]!r} want16 {want16[i]!r} ulp {ulp[i]!r}")
+    else:
+        np.testing.assert_allclose(got.cpu().numpy(), want, atol=3e-6 * np.sqrt(K / 128), rtol=2e-6)
