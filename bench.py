@@ -55,6 +55,10 @@ def parse_args():
                    help="seconds of CPU-oracle timing for the baseline")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--graph", default="auto", choices=["auto", "off", "always"])
+    p.add_argument("--traffic", default="pmc", choices=["pmc", "off"],
+                   help="HBM bytes of the dominant kernel from two rocprofv3 --pmc child runs")
+    p.add_argument("--profile-ops", default=None, metavar="OP",
+                   help="(child mode for --pmc) run one op of the layer and the copy, then exit")
     return p.parse_args()
 
 
@@ -113,10 +117,13 @@ def device_us(fn, reps, replays=5):
     return us
 
 
-def kernel_table(cfg, model, x, mask, reps):
-    """Time each kernel of the layer alone (HIP events on the launch stream).
+def layer_ops(cfg, model, x, mask):
+    """Every kernel launch of one layer forward, as separately callable ops.
 
-    Returns name -> dict(us, flops or bytes, achieved, unit, frac, bound).
+    Returns name -> (fn, bound, algorithmic work per call, compulsory HBM
+    bytes per call): work is flops for the MFMA kernels, HBM bytes for the
+    LayerNorms. The intermediate tensors the
+    ops read are produced once here, by the same kernels.
     """
     import torch
 
@@ -129,7 +136,6 @@ def kernel_table(cfg, model, x, mask, reps):
     T = B * S
     layer = model.layers[0]
     attn = layer.attention
-    dev = x.device
     mask_np = None if mask is None else mask.cpu().numpy()
     L = lengths_of(mask_np, cfg, B)
 
@@ -148,47 +154,171 @@ def kernel_table(cfg, model, x, mask, reps):
         hidden = kx.linear_gelu(n2, layer.ffn_in.weight, layer.ffn_in.bias, -1, -1, True)
         ffn = kx.linear_bias(hidden, layer.ffn_out.weight, layer.ffn_out.bias)
 
-        ops = {
-            "layernorm (norm1, split-fp16 out)": (
-                lambda: kx.fused_layernorm_split(x2, layer.norm1.weight, layer.norm1.bias),
-                "hbm", T * D * 8.0),
-            "linear qkv (fp16x3, fp16 out)": (
-                lambda: kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True),
-                "mfma", 2.0 * T * D * 3 * D),
-            "attention": (
-                lambda: kx.fused_attention_forward(q, k, v, amask, cfg.causal, hd ** -0.5, 0, 1, 0),
-                "mfma", attention_useful_flops(cfg, L)),
-            "linear out_proj": (
-                lambda: kx.linear_bias(ctx2, attn.out_proj.weight, attn.out_proj.bias),
-                "mfma", 2.0 * T * D * D),
-            "add+layernorm (norm2, fp16 out)": (
-                lambda: kx.fused_add_layernorm(x2, attn_out, layer.norm2.weight,
-                                               layer.norm2.bias, 1e-5, True),
-                "hbm", T * D * 14.0),
-            "linear_gelu ffn_in (fp16 out)": (
-                lambda: kx.linear_gelu(n2, layer.ffn_in.weight, layer.ffn_in.bias, -1, -1, True),
-                "mfma", 2.0 * T * D * F),
-            "linear ffn_out": (
-                lambda: kx.linear_bias(hidden, layer.ffn_out.weight, layer.ffn_out.bias),
-                "mfma", 2.0 * T * F * D),
-            "add+layernorm (final, fp32 out)": (
-                lambda: kx.fused_add_layernorm(x2, ffn, model.final_norm.weight,
-                                               model.final_norm.bias, 1e-5, False),
-                "hbm", T * D * 16.0),
-        }
-        out = {}
-        for name, (fn, bound, work) in ops.items():
+    def nb(*ts):
+        return float(sum(t.numel() * t.element_size() for t in ts if t is not None))
+
+    # Compulsory HBM bytes per call: every operand read once, every output
+    # written once (the fp16 weight copies the GEMMs read; the split QKV
+    # weight is two fp16 planes).
+    wq16 = 2.0 * 2 * qkv_w.numel()
+    w16 = lambda lin: 2.0 * lin.weight.numel() + nb(lin.bias)  # noqa: E731
+    ops = {
+        "layernorm (norm1, split-fp16 out)": (
+            lambda: kx.fused_layernorm_split(x2, layer.norm1.weight, layer.norm1.bias),
+            "hbm", T * D * 8.0, nb(x2, planes)),
+        "linear qkv (fp16x3, fp16 out)": (
+            lambda: kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True),
+            "mfma", 2.0 * T * D * 3 * D, nb(planes, qkv_b, qkv) + wq16),
+        "attention": (
+            lambda: kx.fused_attention_forward(q, k, v, amask, cfg.causal, hd ** -0.5, 0, 1, 0),
+            "mfma", attention_useful_flops(cfg, L), nb(qkv, mask, ctx)),
+        "linear out_proj": (
+            lambda: kx.linear_bias(ctx2, attn.out_proj.weight, attn.out_proj.bias),
+            "mfma", 2.0 * T * D * D, nb(ctx2, attn_out) + w16(attn.out_proj)),
+        "add+layernorm (norm2, fp16 out)": (
+            lambda: kx.fused_add_layernorm(x2, attn_out, layer.norm2.weight,
+                                           layer.norm2.bias, 1e-5, True),
+            "hbm", T * D * 14.0, T * D * 14.0),
+        "linear_gelu ffn_in (fp16 out)": (
+            lambda: kx.linear_gelu(n2, layer.ffn_in.weight, layer.ffn_in.bias, -1, -1, True),
+            "mfma", 2.0 * T * D * F, nb(n2, hidden) + w16(layer.ffn_in)),
+        "linear ffn_out": (
+            lambda: kx.linear_bias(hidden, layer.ffn_out.weight, layer.ffn_out.bias),
+            "mfma", 2.0 * T * F * D, nb(hidden, ffn) + w16(layer.ffn_out)),
+        "add+layernorm (final, fp32 out)": (
+            lambda: kx.fused_add_layernorm(x2, ffn, model.final_norm.weight,
+                                           model.final_norm.bias, 1e-5, False),
+            "hbm", T * D * 16.0, T * D * 16.0),
+    }
+    return ops
+
+
+def kernel_table(cfg, model, x, mask, reps):
+    """Time each kernel of the layer alone (HIP events on the launch stream).
+
+    Returns name -> dict(us, flops or bytes, achieved, unit, frac, bound).
+    """
+    import torch
+
+    out = {}
+    with torch.inference_mode():
+        for name, (fn, bound, work, io_bytes) in layer_ops(cfg, model, x, mask).items():
             us = device_us(fn, reps)
             if bound == "mfma":
                 achieved = work / (us * 1e-6) / 1e12
-                out[name] = dict(us=us, flops=work, bound="mfma", achieved=achieved,
+                out[name] = dict(us=us, flops=work, io_bytes=io_bytes, bound="mfma",
+                                 achieved=achieved,
                                  unit="TFLOP/s", peak=PEAK_MFMA_TFLOPS,
                                  frac=achieved / PEAK_MFMA_TFLOPS)
             else:
                 achieved = work / (us * 1e-6) / 1e9
-                out[name] = dict(us=us, bytes=work, bound="hbm", achieved=achieved,
+                out[name] = dict(us=us, bytes=work, io_bytes=io_bytes, bound="hbm",
+                                 achieved=achieved,
                                  unit="GB/s", peak=PEAK_HBM_GBS, frac=achieved / PEAK_HBM_GBS)
     return out
+
+
+# Kernel-symbol substring of each op family (the --pmc CSV names dispatches
+# by symbol), and the calibration copy: dotl_smoke_test_identity over
+# COPY_FLOATS floats reads and writes exactly 4 * COPY_FLOATS bytes.
+KERNEL_FAMILY = (("attention", "attn_fwd"), ("linear", "gemm"), ("layernorm", "layernorm"))
+COPY_SYMBOL = "identity_kernel"
+COPY_FLOATS = 64 << 20
+PROFILE_REPS = 5
+
+
+def kernel_family(op_name):
+    for prefix, symbol in KERNEL_FAMILY:
+        if op_name.startswith(prefix) or prefix in op_name:
+            return symbol
+    raise KeyError(op_name)
+
+
+def profile_ops(args):
+    """Child mode for the --pmc passes: one op PROFILE_REPS times, then the copy.
+
+    The op's inputs come from the layer's own kernels; the last PROFILE_REPS
+    dispatches of the op's kernel family are the op alone.
+    """
+    import torch
+
+    import kernel_ext
+    from layer_runner import TransformerConfig, build_model, to_device
+    from oracle.inputs import CONFIGS, make_case
+
+    cfg = CONFIGS[args.config]
+    x_np, mask_np, params = make_case(cfg)
+    tcfg = TransformerConfig(cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads,
+                             cfg.ffn_dim, 1, cfg.causal)
+    model = build_model(tcfg, params)
+    x, mask = to_device(x_np, mask_np)
+    fn = layer_ops(cfg, model, x, mask)[args.profile_ops][0]
+    with torch.inference_mode():
+        for _ in range(PROFILE_REPS):
+            fn()
+        torch.cuda.synchronize()
+        src = torch.ones(COPY_FLOATS, device=x.device)
+        for _ in range(PROFILE_REPS):
+            kernel_ext.get_kernels().smoke_test_identity(src)
+        torch.cuda.synchronize()
+    return 0
+
+
+def _pmc_pass(counter, op_name, config, outdir):
+    """Mean per-dispatch `counter` (KiB) of the op and of the copy, from a child run."""
+    import csv
+    import glob
+    import subprocess
+
+    cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", outdir,
+           "-o", counter, "--", sys.executable, os.path.abspath(__file__),
+           "--config", config, "--profile-ops", op_name]
+    subprocess.run(cmd, check=True, timeout=180, stdout=subprocess.DEVNULL,
+                   stderr=subprocess.DEVNULL, cwd=REPO)
+    files = glob.glob(os.path.join(outdir, "**", f"{counter}_counter_collection.csv"),
+                      recursive=True)
+    if not files:
+        raise RuntimeError(f"no {counter} counter file under {outdir}")
+    rows = list(csv.DictReader(open(files[0])))
+    fam = kernel_family(op_name)
+
+    def mean_last(symbol):
+        vals = [(int(r["Dispatch_Id"]), float(r["Counter_Value"])) for r in rows
+                if symbol in r["Kernel_Name"] and r["Counter_Name"] == counter]
+        vals = sorted(vals)[-PROFILE_REPS:]
+        if len(vals) < PROFILE_REPS:
+            raise RuntimeError(f"{counter}: {len(vals)} dispatches of {symbol}")
+        return sum(v for _, v in vals) / len(vals)
+
+    return mean_last(fam), mean_last(COPY_SYMBOL)
+
+
+def measure_traffic(op_name, config):
+    """HBM bytes per launch of `op_name` from two rocprofv3 --pmc passes.
+
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are each scaled by what the
+    same counter reads for the calibration copy, whose true traffic is
+    4 * COPY_FLOATS bytes each way. Returns (bytes, detail) or (None, reason).
+    """
+    import shutil
+    import tempfile
+
+    if shutil.which("rocprofv3") is None:
+        return None, "rocprofv3 not on PATH"
+    outdir = tempfile.mkdtemp(prefix="dotl_pmc_")
+    try:
+        op_rd, copy_rd = _pmc_pass("FETCH_SIZE", op_name, config, outdir)
+        op_wr, copy_wr = _pmc_pass("WRITE_SIZE", op_name, config, outdir)
+    except Exception as e:  # the figure is optional; the bench line is not
+        return None, f"pmc pass failed: {e}"
+    finally:
+        shutil.rmtree(outdir, ignore_errors=True)
+    true_bytes = 4.0 * COPY_FLOATS
+    f_rd = true_bytes / (copy_rd * 1024.0)
+    f_wr = true_bytes / (copy_wr * 1024.0)
+    traffic = op_rd * 1024.0 * f_rd + op_wr * 1024.0 * f_wr
+    return traffic, {"fetch_kib": round(op_rd, 1), "write_kib": round(op_wr, 1),
+                     "fetch_scale": round(f_rd, 4), "write_scale": round(f_wr, 4)}
 
 
 def cpu_baseline(cfg, x_np, mask_np, params, budget_s):
@@ -251,12 +381,25 @@ def run_config(name, steps, warmup, graph, with_kernels=True):
 
 
 def main():
+    # The package's [info] lines (graph capture notes) go to stderr: stdout
+    # carries exactly one line, the JSON result.
+    real_stdout = sys.stdout
+    sys.stdout = sys.stderr
+    try:
+        return _main(real_stdout)
+    finally:
+        sys.stdout = real_stdout
+
+
+def _main(out):
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (--gpus {args.gpus} "
               f"was asked for). The layer shards by batch with no exchange; see DESIGN.md.",
               file=sys.stderr)
         return 2
+    if args.profile_ops:
+        return profile_ops(args)
     import torch
 
     import kernel_ext
@@ -280,6 +423,12 @@ def main():
     dom = kt[dom_name]
     attn = kt["attention"]
     ln = kt["add+layernorm (final, fp32 out)"]
+
+    traffic, traffic_detail = None, "not measured (--traffic off)"
+    if args.traffic == "pmc":
+        log(f"[bench] HBM traffic of '{dom_name}' from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE ...")
+        traffic, traffic_detail = measure_traffic(dom_name, args.config)
+        log(f"[bench] traffic {traffic} bytes/launch ({traffic_detail})")
 
     cpu = None
     if not args.no_cpu:
@@ -309,7 +458,10 @@ def main():
         "layer_tflops": round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 2),
         "roofline": {"bound": dom["bound"], "kernel": dom_name,
                      "achieved": round(dom["achieved"], 2), "peak": dom["peak"],
-                     "unit": dom["unit"], "frac": round(dom["frac"], 4), "traffic": None},
+                     "unit": dom["unit"], "frac": round(dom["frac"], 4),
+                     "traffic": None if traffic is None else round(traffic),
+                     "traffic_detail": traffic_detail,
+                     "compulsory_bytes": round(dom["io_bytes"])},
         "attn_mfma_util_pct": round(100 * attn["frac"], 2),
         "ln_hbm_gbs": round(ln["achieved"], 1),
         "kernels": {k: {"us": round(v["us"], 2), "achieved": round(v["achieved"], 2),
@@ -317,7 +469,7 @@ def main():
         "cpu_baseline": cpu,
         "speedup_vs_cpu": (round(cpu["value"] / us, 1) if cpu else None),
     }
-    print(json.dumps(line), flush=True)
+    print(json.dumps(line), file=out, flush=True)
 
     if args.all:
         log("[bench] per-config table (graph replay / eager us, layer TFLOP/s)")
