@@ -6,8 +6,10 @@ over one synthetic batch already resident in HBM.
 
 Workload: BASELINE config 1 (the padded batch: B=8, S=512, d_model=512,
 8 heads, d_ff=2048, key-padding mask), Xavier weights from the fixed seed.
-`--config C1..C5` selects another config; `--all` adds a per-config table on
-stderr.
+`--config C1..C5` selects another config. Unless --quick, the line also carries
+a per-config table (C1..C5: layer µs, CPU-oracle µs, speedup, attention MFMA
+utilisation, final add+LN GB/s) and the geomean speedup over the five
+configs, the metric's second figure.
 
 Reported beside the layer time:
   roofline      the dominant kernel of the layer, timed alone with HIP events
@@ -50,7 +52,8 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
-    p.add_argument("--all", action="store_true", help="also time every config (stderr table)")
+    p.add_argument("--quick", action="store_true",
+                   help="skip the per-config table (C1..C5 layer µs and CPU speedups)")
     p.add_argument("--cpu-budget", type=float, default=20.0,
                    help="seconds of CPU-oracle timing for the baseline")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -436,6 +439,34 @@ def _main(out):
         cpu = cpu_baseline(cfg, r["x_np"], r["mask_np"], r["params"], args.cpu_budget)
         log(f"[bench] cpu baseline {cpu['value']:.0f} us on {cpu['cores']} threads")
 
+    per_config, geomean = {}, None
+    if not args.quick:
+        log("[bench] per-config table: layer µs (graph replay), CPU oracle µs, attention MFMA %, "
+            "final add+LN GB/s")
+        speedups = []
+        for name in ["C1", "C2", "C3", "C4", "C5"]:
+            rr = r if name == args.config else run_config(name, max(10, args.steps // 2), 3,
+                                                          args.graph)
+            k = rr["kernels"]
+            entry = {"us": round(rr["ms"] * 1000.0, 2), "eager_us": round(rr["ms_eager"] * 1000.0, 2),
+                     "layer_tflops": round(rr["flops"] / (rr["ms"] * 1e-3) / 1e12, 2),
+                     "attn_mfma_util_pct": round(100 * k["attention"]["frac"], 2),
+                     "ln_hbm_gbs": round(k["add+layernorm (final, fp32 out)"]["achieved"], 1)}
+            if not args.no_cpu:
+                c = cpu if (name == args.config and cpu) else cpu_baseline(
+                    rr["config"], rr["x_np"], rr["mask_np"], rr["params"], args.cpu_budget / 3)
+                entry["cpu_us"] = round(c["value"], 1)
+                entry["speedup_vs_cpu"] = round(c["value"] / (rr["ms"] * 1000.0), 2)
+                speedups.append(entry["speedup_vs_cpu"])
+            per_config[name] = entry
+            log(f"[bench] {name}: {entry}")
+            if rr is not r:
+                del rr
+                torch.cuda.empty_cache()
+        if speedups and len(speedups) == 5:
+            geomean = round(math.exp(sum(math.log(v) for v in speedups) / len(speedups)), 2)
+            log(f"[bench] geomean speedup vs CPU oracle over C1..C5: {geomean}x")
+
     line = {
         "metric": "layer fwd µs/geomean speedup vs CPU ref; attn MFMA util %, LN HBM GB/s",
         "value": round(us, 2),
@@ -469,19 +500,10 @@ def _main(out):
         "cpu_baseline": cpu,
         "speedup_vs_cpu": (round(cpu["value"] / us, 1) if cpu else None),
     }
+    if per_config:
+        line["per_config"] = per_config
+        line["geomean_speedup_vs_cpu"] = geomean
     print(json.dumps(line), file=out, flush=True)
-
-    if args.all:
-        log("[bench] per-config table (graph replay / eager us, layer TFLOP/s)")
-        for name in ["C1", "C2", "C3", "C4", "C5"]:
-            rr = run_config(name, max(5, args.steps // 2), 3, args.graph, with_kernels=True)
-            k = rr["kernels"]
-            log(f"[bench] {name}: {rr['ms'] * 1000:.1f} us (eager {rr['ms_eager'] * 1000:.1f}) "
-                f"layer {rr['flops'] / (rr['ms'] * 1e-3) / 1e12:.1f} TFLOP/s, attention "
-                f"{100 * k['attention']['frac']:.1f}% MFMA, final add+LN "
-                f"{k['add+layernorm (final, fp32 out)']['achieved']:.0f} GB/s")
-            del rr
-            torch.cuda.empty_cache()
     return 0
 
 
