@@ -123,14 +123,18 @@ def device_us(fn, reps, replays=5):
 def layer_ops(cfg, model, x, mask):
     """Every kernel launch of one layer forward, as separately callable ops.
 
-    Returns name -> (fn, bound, algorithmic work per call, compulsory HBM
-    bytes per call): work is flops for the MFMA kernels, HBM bytes for the
-    LayerNorms. The intermediate tensors the
-    ops read are produced once here, by the same kernels.
+    Follows the path the model takes: on a padded batch with row packing on
+    (the default), the first LayerNorm gathers the T_valid valid rows, the
+    GEMMs and attention run on them, and the final add+LayerNorm scatters
+    back to B*S rows. Returns name -> (fn, bound, algorithmic work per call,
+    compulsory HBM bytes per call): work is flops for the MFMA kernels, HBM
+    bytes for the LayerNorms. The intermediate tensors the ops read are
+    produced once here, by the same kernels.
     """
     import torch
 
     import kernel_ext
+    from optimized import config as ocfg
     from oracle.inputs import attention_useful_flops, lengths_of
 
     kx = kernel_ext.get_kernels()
@@ -141,21 +145,49 @@ def layer_ops(cfg, model, x, mask):
     attn = layer.attention
     mask_np = None if mask is None else mask.cpu().numpy()
     L = lengths_of(mask_np, cfg, B)
+    packing = model._mask_packing(mask) if mask is not None else None
+    if packing is not None and (packing.trivial or ocfg.ROW_PACKING == "off"):
+        packing = None
+    R = packing.t_valid if packing is not None else T   # rows the GEMMs see
+    scale = hd ** -0.5
+    fw, fb = model.final_norm.weight, model.final_norm.bias
 
     with torch.inference_mode():
-        x2 = x.reshape(T, D)
-        planes = kx.fused_layernorm_split(x2, layer.norm1.weight, layer.norm1.bias)
+        if packing is not None:
+            ln1 = lambda: kx.fused_layernorm_rows(x, layer.norm1.weight, layer.norm1.bias,  # noqa: E731
+                                                  packing.idx, 1e-5, "split", True)
+            x2, planes = ln1()
+            ln1_bytes = R * D * 12.0            # read x, write the gathered x and the planes
+        else:
+            x2 = x.reshape(T, D)
+            ln1 = lambda: kx.fused_layernorm_split(x2, layer.norm1.weight, layer.norm1.bias)  # noqa: E731
+            planes = ln1()
+            ln1_bytes = T * D * 8.0
         qkv_w, qkv_b = attn._get_qkv_weight()
         qkv = kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True)
-        q, k, v = qkv.view(B, S, 3, H, hd).permute(2, 0, 3, 1, 4).unbind(0)
-        amask = None if mask is None else mask[:, None, None, :]
-        ctx = kx.fused_attention_forward(q, k, v, amask, cfg.causal, hd ** -0.5, 0, 1, 0)
-        ctx2 = ctx.reshape(T, D)
+        if packing is not None:
+            q, k, v = qkv.view(R, 3, H, hd).unbind(1)
+            attn_fn = lambda: kx.fused_attention_forward(q, k, v, None, cfg.causal, scale, 0, 1, 0,  # noqa: E731
+                                                         cu_seqlens=packing.cu, max_seqlen=S)
+            amask = None
+        else:
+            q, k, v = qkv.view(B, S, 3, H, hd).permute(2, 0, 3, 1, 4).unbind(0)
+            amask = None if mask is None else mask[:, None, None, :]
+            attn_fn = lambda: kx.fused_attention_forward(q, k, v, amask, cfg.causal, scale,  # noqa: E731
+                                                         0, 1, 0)
+        ctx = attn_fn()
+        ctx2 = ctx.reshape(R, D)
         attn_out = kx.linear_bias(ctx2, attn.out_proj.weight, attn.out_proj.bias)
-        _, n2 = kx.fused_add_layernorm(x2, attn_out, layer.norm2.weight, layer.norm2.bias,
-                                       1e-5, True)
+        h1, n2 = kx.fused_add_layernorm(x2, attn_out, layer.norm2.weight, layer.norm2.bias,
+                                        1e-5, True)
         hidden = kx.linear_gelu(n2, layer.ffn_in.weight, layer.ffn_in.bias, -1, -1, True)
         ffn = kx.linear_bias(hidden, layer.ffn_out.weight, layer.ffn_out.bias)
+        if packing is not None:
+            final = lambda: kx.fused_add_layernorm_rows(h1, ffn, fw, fb, packing.inv, 1e-5)  # noqa: E731
+            final_bytes = R * D * 8.0 + T * D * 4.0   # read two packed inputs, write B*S rows
+        else:
+            final = lambda: kx.fused_add_layernorm(x2, ffn, fw, fb, 1e-5, False)  # noqa: E731
+            final_bytes = T * D * 16.0
 
     def nb(*ts):
         return float(sum(t.numel() * t.element_size() for t in ts if t is not None))
@@ -165,33 +197,27 @@ def layer_ops(cfg, model, x, mask):
     # weight is two fp16 planes).
     wq16 = 2.0 * 2 * qkv_w.numel()
     w16 = lambda lin: 2.0 * lin.weight.numel() + nb(lin.bias)  # noqa: E731
+    cu_bytes = nb(packing.cu) if packing is not None else nb(mask)
     ops = {
-        "layernorm (norm1, split-fp16 out)": (
-            lambda: kx.fused_layernorm_split(x2, layer.norm1.weight, layer.norm1.bias),
-            "hbm", T * D * 8.0, nb(x2, planes)),
+        "layernorm (norm1, split-fp16 out)": (ln1, "hbm", ln1_bytes, ln1_bytes),
         "linear qkv (fp16x3, fp16 out)": (
             lambda: kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True),
-            "mfma", 2.0 * T * D * 3 * D, nb(planes, qkv_b, qkv) + wq16),
-        "attention": (
-            lambda: kx.fused_attention_forward(q, k, v, amask, cfg.causal, hd ** -0.5, 0, 1, 0),
-            "mfma", attention_useful_flops(cfg, L), nb(qkv, mask, ctx)),
+            "mfma", 2.0 * R * D * 3 * D, nb(planes, qkv_b, qkv) + wq16),
+        "attention": (attn_fn, "mfma", attention_useful_flops(cfg, L), nb(qkv, ctx) + cu_bytes),
         "linear out_proj": (
             lambda: kx.linear_bias(ctx2, attn.out_proj.weight, attn.out_proj.bias),
-            "mfma", 2.0 * T * D * D, nb(ctx2, attn_out) + w16(attn.out_proj)),
+            "mfma", 2.0 * R * D * D, nb(ctx2, attn_out) + w16(attn.out_proj)),
         "add+layernorm (norm2, fp16 out)": (
             lambda: kx.fused_add_layernorm(x2, attn_out, layer.norm2.weight,
                                            layer.norm2.bias, 1e-5, True),
-            "hbm", T * D * 14.0, T * D * 14.0),
+            "hbm", R * D * 14.0, R * D * 14.0),
         "linear_gelu ffn_in (fp16 out)": (
             lambda: kx.linear_gelu(n2, layer.ffn_in.weight, layer.ffn_in.bias, -1, -1, True),
-            "mfma", 2.0 * T * D * F, nb(n2, hidden) + w16(layer.ffn_in)),
+            "mfma", 2.0 * R * D * F, nb(n2, hidden) + w16(layer.ffn_in)),
         "linear ffn_out": (
             lambda: kx.linear_bias(hidden, layer.ffn_out.weight, layer.ffn_out.bias),
-            "mfma", 2.0 * T * F * D, nb(hidden, ffn) + w16(layer.ffn_out)),
-        "add+layernorm (final, fp32 out)": (
-            lambda: kx.fused_add_layernorm(x2, ffn, model.final_norm.weight,
-                                           model.final_norm.bias, 1e-5, False),
-            "hbm", T * D * 16.0, T * D * 16.0),
+            "mfma", 2.0 * R * F * D, nb(hidden, ffn) + w16(layer.ffn_out)),
+        "add+layernorm (final, fp32 out)": (final, "hbm", final_bytes, final_bytes),
     }
     return ops
 

@@ -78,6 +78,7 @@ struct AttnParams {
     int64_t sb, sh, ss;          // q/k/v strides (elements): batch, head, seq
     const uint8_t* mask;         // nullable
     int64_t mb, mh, mq, mk;      // mask strides (elements)
+    const int32_t* cu;           // nullable: sequence b is rows [cu[b], cu[b+1]) (packed rows)
     void* out;
     int out_layout;              // 0 [B,H,S,hd], 1 [B,S,H*hd]
     int B, H, S;
@@ -119,16 +120,29 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
     const int q_w0 = q_wg0 + wave * 32;   // this wavefront's first query
     const int my_q = q_w0 + lr;           // the query this lane's column is
 
-    const T* qbase = static_cast<const T*>(p.q) + b * p.sb + h * p.sh;
-    const T* kbase = static_cast<const T*>(p.k) + b * p.sb + h * p.sh;
-    const T* vbase = static_cast<const T*>(p.v) + b * p.sb + h * p.sh;
+    // Packed rows: this sequence's length and first row. p.S is then the
+    // longest sequence (the grid's size); a block past this one's end exits
+    // before any barrier, uniformly.
+    int S = p.S;
+    int64_t seq_off = static_cast<int64_t>(b) * p.sb;
+    int64_t row0 = 0;
+    if (p.cu != nullptr) {
+        row0 = p.cu[b];
+        S = p.cu[b + 1] - static_cast<int>(row0);
+        seq_off = row0 * p.ss;
+        if (q_wg0 >= S) return;
+    }
+
+    const T* qbase = static_cast<const T*>(p.q) + seq_off + h * p.sh;
+    const T* kbase = static_cast<const T*>(p.k) + seq_off + h * p.sh;
+    const T* vbase = static_cast<const T*>(p.v) + seq_off + h * p.sh;
 
     // Q^T fragments for the whole key loop: lane supplies Q[my_q][ks*16 + lg*8 .. +8].
     half8 qf[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         qf[ks] = half8{};
-        if (my_q < p.S) qf[ks] = load8<IN_F32>(qbase + static_cast<int64_t>(my_q) * p.ss + ks * 16 + lg * 8);
+        if (my_q < S) qf[ks] = load8<IN_F32>(qbase + static_cast<int64_t>(my_q) * p.ss + ks * 16 + lg * 8);
     }
 
     const bool has_mask = p.mask != nullptr;
@@ -136,15 +150,15 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
     const uint8_t* mbase = has_mask ? p.mask + b * p.mb + h * p.mh : nullptr;
 
     // Key range this workgroup visits.
-    int kend = p.S;
-    if (p.causal) kend = min(p.S, q_wg0 + BM);
+    int kend = S;
+    if (p.causal) kend = min(S, q_wg0 + BM);
     const int nkt = (kend + kBN - 1) / kBN;
 
     // Live-tile test for a key-only mask: any allowed key in the tile.
     auto tile_live = [&](int kt) -> bool {
         if (!key_only_mask) return true;
         const int key = kt * kBN + lane;
-        const bool ok = key < p.S && mbase[static_cast<int64_t>(key) * p.mk] != 0;
+        const bool ok = key < S && mbase[static_cast<int64_t>(key) * p.mk] != 0;
         return __ballot(ok) != 0ull;
     };
 
@@ -166,7 +180,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
             const int row = c / (HD / 8);
             const int col = (c % (HD / 8)) * 8;
             rk[i] = half8{};
-            if (c < KCH && key0 + row < p.S)
+            if (c < KCH && key0 + row < S)
                 rk[i] = load8<IN_F32>(kbase + static_cast<int64_t>(key0 + row) * p.ss + col);
         }
 #pragma unroll
@@ -178,13 +192,13 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
             rv1[i] = half8{};
             if (it < VIT) {
                 const int k0 = key0 + 2 * kp;
-                if (k0 < p.S) rv0[i] = load8<IN_F32>(vbase + static_cast<int64_t>(k0) * p.ss + ch * 8);
-                if (k0 + 1 < p.S) rv1[i] = load8<IN_F32>(vbase + static_cast<int64_t>(k0 + 1) * p.ss + ch * 8);
+                if (k0 < S) rv0[i] = load8<IN_F32>(vbase + static_cast<int64_t>(k0) * p.ss + ch * 8);
+                if (k0 + 1 < S) rv1[i] = load8<IN_F32>(vbase + static_cast<int64_t>(k0 + 1) * p.ss + ch * 8);
             }
         }
         if (key_only_mask && threadIdx.x < kBN) {
             const int key = key0 + threadIdx.x;
-            rm = (key < p.S) ? mbase[static_cast<int64_t>(key) * p.mk] : 0;
+            rm = (key < S) ? mbase[static_cast<int64_t>(key) * p.mk] : 0;
         }
     };
 
@@ -253,7 +267,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
             }
 
             // Scale into the log2 domain, then mask where this tile needs it.
-            const bool full = key0 + kBN <= p.S;
+            const bool full = key0 + kBN <= S;
             const bool diag = p.causal && key0 + kBN - 1 > q_w0;
             const bool needs_test = !full || diag || has_mask;
             float tmax = -INFINITY;
@@ -265,12 +279,12 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
                     if (needs_test) {
                         const int kl = t2 * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
                         const int key = key0 + kl;
-                        bool ok = key < p.S;
+                        bool ok = key < S;
                         if (p.causal) ok = ok && key <= my_q;
                         if (has_mask) {
                             if (key_only_mask) {
                                 ok = ok && sMask[kl] != 0;
-                            } else if (ok && my_q < p.S) {
+                            } else if (ok && my_q < S) {
                                 ok = mbase[static_cast<int64_t>(my_q) * p.mq +
                                            static_cast<int64_t>(key) * p.mk] != 0;
                             }
@@ -329,11 +343,13 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
     // 32*j + 8*(r/4) + 4*g + r%4, query column l%32.
     const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-    if (my_q < p.S) {
+    if (my_q < S) {
         const int64_t obase =
-            p.out_layout == 1
-                ? ((static_cast<int64_t>(b) * p.S + my_q) * p.H + h) * HD
-                : ((static_cast<int64_t>(b) * p.H + h) * p.S + my_q) * HD;
+            p.cu != nullptr
+                ? ((row0 + my_q) * p.H + h) * HD
+                : (p.out_layout == 1
+                       ? ((static_cast<int64_t>(b) * S + my_q) * p.H + h) * HD
+                       : ((static_cast<int64_t>(b) * p.H + h) * S + my_q) * HD);
 #pragma unroll
         for (int j = 0; j < HT; ++j) {
 #pragma unroll
@@ -416,7 +432,7 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
                                       const int64_t* mask_strides, void* out, int out_dtype,
                                       int out_layout, int B, int H, int S, int head_dim,
                                       int is_causal, double scale, int impl, int precision,
-                                      void* stream) {
+                                      const int32_t* cu_seqlens, void* stream) {
     using namespace dotl;
     clear_error();
     DOTL_REQUIRE(out_layout == 0 || out_layout == 1,
@@ -469,6 +485,9 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
     DOTL_REQUIRE(q && k && v && out, "fused_attention_forward: null pointer");
     DOTL_REQUIRE(mask == nullptr || mask_strides != nullptr,
                  "fused_attention_forward: mask strides required with a mask");
+    DOTL_REQUIRE(cu_seqlens == nullptr || (mask == nullptr && out_layout == 1),
+                 "fused_attention_forward: packed sequences (cu_seqlens) take no mask and "
+                 "write the packed [rows, H*head_dim] layout (out_layout 1)");
     const int64_t es = dtype == DOTL_F16 ? 2 : 4;
     const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                             reinterpret_cast<uintptr_t>(v) |
@@ -486,6 +505,7 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
         p.mb = mask_strides[0]; p.mh = mask_strides[1];
         p.mq = mask_strides[2]; p.mk = mask_strides[3];
     }
+    p.cu = cu_seqlens;
     p.out = out;
     p.out_layout = out_layout;
     p.B = B; p.H = H; p.S = S;

@@ -1,5 +1,11 @@
 // Residual add + LayerNorm, and plain LayerNorm, for gfx950.
 //
+// Optional row index (the packed-row path of a padded batch): output row t
+// reads input row row_index[t] of x and sub -- a gather when the output
+// holds the packed valid rows, a scatter-back when it holds the padded
+// layout -- and an entry outside [0, in_rows) writes zeros to every output
+// of row t (the padded rows the reference zeroes with masked_fill).
+//
 // Replaces fused_add_layernorm / fused_layernorm (reference
 // csrc/add_layernorm.cuh:491-692). Same contract: x_new = x + sub, normed =
 // (x_new - mean) * rsqrt(var + eps) * w + b with the biased variance, fp32
@@ -29,6 +35,8 @@ namespace {
 
 constexpr int kRowsPerBlock = 4;
 
+__device__ __forceinline__ int64_t D_of(int nchunk) { return 4 * static_cast<int64_t>(nchunk); }
+
 template <bool HAS_SUB>
 __device__ __forceinline__ float4 load_sum4(const float* __restrict__ x,
                                             const float* __restrict__ sub, int64_t off) {
@@ -40,6 +48,29 @@ __device__ __forceinline__ float4 load_sum4(const float* __restrict__ x,
     return a;
 }
 
+// A row whose index entry is negative: every output of the row is zero.
+template <int CH, bool WRITE_XNEW, int NORMED>
+__device__ __forceinline__ void zero_row_vec(float* __restrict__ x_new, void* __restrict__ normed,
+                                             int64_t rows, int64_t base, int nchunk, int lane) {
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int idx = c * 64 + lane;
+        if (idx < nchunk) {
+            const int col = 4 * idx;
+            if constexpr (WRITE_XNEW) *reinterpret_cast<float4*>(x_new + base + col) = z;
+            if constexpr (NORMED == DOTL_F16 || NORMED == DOTL_F16X2) {
+                const half4 hz = {};
+                *reinterpret_cast<half4*>(static_cast<_Float16*>(normed) + base + col) = hz;
+                if constexpr (NORMED == DOTL_F16X2)
+                    *reinterpret_cast<half4*>(static_cast<_Float16*>(normed) + rows * D_of(nchunk) + base + col) = hz;
+            } else {
+                *reinterpret_cast<float4*>(static_cast<float*>(normed) + base + col) = z;
+            }
+        }
+    }
+}
+
 // Vector path: D % 4 == 0 and D <= 256 * CH. Chunk c of lane l covers row
 // elements [4 * (c * 64 + l), +4).
 template <int CH, bool HAS_SUB, bool WRITE_XNEW, int NORMED>
@@ -47,7 +78,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     const float* __restrict__ x, const float* __restrict__ sub,
     const float* __restrict__ w, const float* __restrict__ b,
     float* __restrict__ x_new, void* __restrict__ normed,
-    int64_t rows, int D, float eps) {
+    const int32_t* __restrict__ row_index, int64_t in_rows, int64_t rows, int D, float eps) {
     const int lane = threadIdx.x & 63;
     const int64_t wave_global = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
     const int64_t wave_stride = static_cast<int64_t>(gridDim.x) * kRowsPerBlock;
@@ -55,14 +86,21 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     const float inv_d = 1.0f / static_cast<float>(D);
 
     for (int64_t row = wave_global; row < rows; row += wave_stride) {
-        const int64_t base = row * D;
+        const int64_t base = row * D;   // output row
+        int64_t src = row_index ? static_cast<int64_t>(row_index[row]) : row;
+        if (src >= in_rows) src = -1;
+        if (src < 0) {
+            zero_row_vec<CH, WRITE_XNEW, NORMED>(x_new, normed, rows, base, nchunk, lane);
+            continue;
+        }
+        const int64_t ibase = src * D;  // input row
         float4 v[CH];
         float s = 0.f;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int idx = c * 64 + lane;
             if (idx < nchunk) {
-                v[c] = load_sum4<HAS_SUB>(x, sub, base + 4 * idx);
+                v[c] = load_sum4<HAS_SUB>(x, sub, ibase + 4 * idx);
             } else {
                 v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
@@ -133,14 +171,34 @@ __global__ __launch_bounds__(256) void layernorm_scalar_kernel(
     const float* __restrict__ x, const float* __restrict__ sub,
     const float* __restrict__ w, const float* __restrict__ b,
     float* __restrict__ x_new, void* __restrict__ normed,
-    int64_t rows, int D, float eps) {
+    const int32_t* __restrict__ row_index, int64_t in_rows, int64_t rows, int D, float eps) {
     const int lane = threadIdx.x & 63;
     const int64_t wave_global = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
     const int64_t wave_stride = static_cast<int64_t>(gridDim.x) * kRowsPerBlock;
     const float inv_d = 1.0f / static_cast<float>(D);
 
     for (int64_t row = wave_global; row < rows; row += wave_stride) {
-        const int64_t base = row * D;
+        const int64_t base = row * D;   // output row
+        int64_t src = row_index ? static_cast<int64_t>(row_index[row]) : row;
+        if (src >= in_rows) src = -1;
+        if (src < 0) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const int col = e * 64 + lane;
+                if (col < D) {
+                    if constexpr (WRITE_XNEW) x_new[base + col] = 0.f;
+                    if constexpr (NORMED == DOTL_F16 || NORMED == DOTL_F16X2) {
+                        static_cast<_Float16*>(normed)[base + col] = static_cast<_Float16>(0.f);
+                        if constexpr (NORMED == DOTL_F16X2)
+                            static_cast<_Float16*>(normed)[rows * D + base + col] = static_cast<_Float16>(0.f);
+                    } else {
+                        static_cast<float*>(normed)[base + col] = 0.f;
+                    }
+                }
+            }
+            continue;
+        }
+        const int64_t ibase = src * D;  // input row
         float v[EPL];
         float s = 0.f;
 #pragma unroll
@@ -148,8 +206,8 @@ __global__ __launch_bounds__(256) void layernorm_scalar_kernel(
             const int col = e * 64 + lane;
             float a = 0.f;
             if (col < D) {
-                a = x[base + col];
-                if constexpr (HAS_SUB) a += sub[base + col];
+                a = x[ibase + col];
+                if constexpr (HAS_SUB) a += sub[ibase + col];
             }
             v[e] = a;
             s += a;
@@ -198,6 +256,8 @@ struct LnArgs {
     const float* b;
     float* x_new;
     void* normed;
+    const int32_t* row_index;
+    int64_t in_rows;
     int64_t rows;
     int D;
     float eps;
@@ -216,14 +276,14 @@ template <int CH, bool HAS_SUB, bool WX, int F16>
 void launch_vec(const LnArgs& a) {
     hipLaunchKernelGGL((layernorm_vec_kernel<CH, HAS_SUB, WX, F16>), dim3(grid_for(a.rows)),
                        dim3(256), 0, a.stream, a.x, a.sub, a.w, a.b, a.x_new, a.normed,
-                       a.rows, a.D, a.eps);
+                       a.row_index, a.in_rows, a.rows, a.D, a.eps);
 }
 
 template <int EPL, bool HAS_SUB, bool WX, int F16>
 void launch_scalar(const LnArgs& a) {
     hipLaunchKernelGGL((layernorm_scalar_kernel<EPL, HAS_SUB, WX, F16>), dim3(grid_for(a.rows)),
                        dim3(256), 0, a.stream, a.x, a.sub, a.w, a.b, a.x_new, a.normed,
-                       a.rows, a.D, a.eps);
+                       a.row_index, a.in_rows, a.rows, a.D, a.eps);
 }
 
 template <bool HAS_SUB, bool WX, int F16>
@@ -249,7 +309,8 @@ void dispatch_width(const LnArgs& a, bool vec) {
 }  // namespace dotl
 
 extern "C" int dotl_layernorm(const void* x, const void* sub, const float* weight,
-                              const float* bias, void* x_new, void* normed, int64_t rows,
+                              const float* bias, void* x_new, void* normed,
+                              const int32_t* row_index, int64_t in_rows, int64_t rows,
                               int64_t D, double eps, int dtype, int normed_dtype,
                               void* stream) {
     using namespace dotl;
@@ -264,8 +325,7 @@ extern "C" int dotl_layernorm(const void* x, const void* sub, const float* weigh
     DOTL_REQUIRE(D >= 1 && D <= 8192, "%s: last dimension %lld outside [1, 8192]", who,
                  static_cast<long long>(D));
     DOTL_REQUIRE(rows >= 0, "%s: negative row count", who);
-    DOTL_REQUIRE(sub != nullptr || x_new == nullptr,
-                 "%s: x_new is only written when a residual is added", who);
+    DOTL_REQUIRE(row_index == nullptr || in_rows >= 0, "%s: negative input row count", who);
     if (rows == 0) return DOTL_OK;
     DOTL_REQUIRE(x && weight && bias && normed, "%s: null pointer", who);
 
@@ -276,7 +336,8 @@ extern "C" int dotl_layernorm(const void* x, const void* sub, const float* weigh
     const bool vec = (D % 4 == 0) && aligned;
 
     LnArgs a{static_cast<const float*>(x), static_cast<const float*>(sub), weight, bias,
-             static_cast<float*>(x_new), normed, rows, static_cast<int>(D),
+             static_cast<float*>(x_new), normed, row_index, row_index ? in_rows : rows, rows,
+             static_cast<int>(D),
              static_cast<float>(eps), as_stream(stream)};
     auto by_out = [&](auto has_sub, auto wx) {
         constexpr bool HS = decltype(has_sub)::value;
@@ -291,7 +352,8 @@ extern "C" int dotl_layernorm(const void* x, const void* sub, const float* weigh
         if (x_new) by_out(std::true_type{}, std::true_type{});
         else by_out(std::true_type{}, std::false_type{});
     } else {
-        by_out(std::false_type{}, std::false_type{});
+        if (x_new) by_out(std::false_type{}, std::true_type{});
+        else by_out(std::false_type{}, std::false_type{});
     }
     return check_launch(who);
 }

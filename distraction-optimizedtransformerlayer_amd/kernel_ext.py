@@ -37,7 +37,7 @@ _THIS_DIR = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_THIS_DIR, "libdotl_hip.so")
 _CSRC = os.path.join(_THIS_DIR, "csrc")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DOTL_OK = 0
 DOTL_DECLINED = 1
@@ -97,7 +97,8 @@ def _declare(lib) -> None:
     lib.dotl_lds_dma_probe.restype = i32
     lib.dotl_lds_dma_probe.argtypes = [vp, vp, vp]
     lib.dotl_layernorm.restype = i32
-    lib.dotl_layernorm.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, c.c_double, i32, i32, vp]
+    lib.dotl_layernorm.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, c.c_double, i32,
+                                   i32, vp]
     lib.dotl_weight_split.restype = i32
     lib.dotl_weight_split.argtypes = [vp, vp, vp, i64, vp]
     lib.dotl_linear.restype = i32
@@ -105,7 +106,7 @@ def _declare(lib) -> None:
     lib.dotl_attention_forward.restype = i32
     lib.dotl_attention_forward.argtypes = [vp, vp, vp, i32, c.POINTER(i64), vp, c.POINTER(i64),
                                            vp, i32, i32, i32, i32, i32, i32, i32, c.c_double,
-                                           i32, i32, vp]
+                                           i32, i32, vp, vp]
     lib.dotl_ffn_block.restype = i32
     lib.dotl_ffn_block.argtypes = [vp] * 12 + [i64, i64, i64, c.c_double, vp]
     lib.dotl_wmma_set_fp16.restype = None
@@ -218,10 +219,17 @@ class Kernels:
     # -- LayerNorm (reference csrc/add_layernorm.cuh:491-692) -----------------------
 
     def _layernorm(self, who, x, sub, weight, bias, eps, normed_half, write_xnew=True,
-                   split=False):
+                   split=False, row_index=None):
+        """Shared body of the LayerNorm methods.
+
+        x_new is written when `write_xnew` and either a residual is added or a
+        row index is given (then it is the gathered x). With `row_index`
+        (int32 [rows], device), x/sub are read as [in_rows, D] and both
+        outputs are [rows, D]; an entry outside [0, in_rows) gives zero rows.
+        """
         import torch
 
-        self._require_cuda(who, x, sub, weight, bias)
+        self._require_cuda(who, x, sub, weight, bias, row_index)
         if x.dim() < 1:
             raise RuntimeError(f"{who}: x needs at least one dimension")
         D = x.shape[-1]
@@ -242,23 +250,60 @@ class Kernels:
         xc = x.contiguous()
         sc = sub.contiguous() if sub is not None else None
         wc, bc = weight.contiguous(), bias.contiguous()
-        x_new = torch.empty_like(xc) if (sc is not None and write_xnew) else None
+        in_rows = xc.numel() // D if D else 0
+        if row_index is not None:
+            if row_index.dtype != torch.int32 or row_index.dim() != 1:
+                raise RuntimeError(f"{who}: row_index must be a 1-D int32 tensor")
+            ri = row_index.contiguous()
+            rows = ri.numel()
+            out_shape = (rows, D)
+        else:
+            ri = None
+            rows = in_rows
+            out_shape = tuple(xc.shape)
+        want_xnew = write_xnew and (sc is not None or ri is not None)
+        x_new = torch.empty(out_shape, dtype=xc.dtype, device=xc.device) if want_xnew else None
         if split:
-            normed = torch.empty((2, *xc.shape), dtype=torch.float16, device=xc.device)
+            normed = torch.empty((2, *out_shape), dtype=torch.float16, device=xc.device)
             ncode = DOTL_F16X2
         else:
-            normed = torch.empty(xc.shape, dtype=torch.float16 if normed_half else torch.float32,
+            normed = torch.empty(out_shape, dtype=torch.float16 if normed_half else torch.float32,
                                  device=xc.device)
             ncode = DOTL_F16 if normed_half else DOTL_F32
-        rows = xc.numel() // D if D else 0
         rc = self._lib.dotl_layernorm(
             xc.data_ptr(), sc.data_ptr() if sc is not None else None, wc.data_ptr(),
             bc.data_ptr(), x_new.data_ptr() if x_new is not None else None, normed.data_ptr(),
-            rows, D, float(eps), DOTL_F32, ncode, self._stream(x.device))
+            ri.data_ptr() if ri is not None else None, in_rows, rows, D, float(eps), DOTL_F32,
+            ncode, self._stream(x.device))
         self._check(rc)
         if rc == DOTL_DECLINED:
             raise RuntimeError(self._err())
         return x_new, normed
+
+    def fused_layernorm_rows(self, x, weight, bias, row_index, eps=1e-5, normed="float",
+                             copy_x=True):
+        """[x[row_index], LayerNorm(x[row_index])]: the gather into packed rows.
+
+        Not in the reference's surface. `x` is [..., D] read as [in_rows, D];
+        `row_index` int32 [rows] on the device; `normed` is "float", "half" or
+        "split" (fp16 hi/lo planes [2, rows, D]); `copy_x` also returns the
+        gathered rows of x (else None).
+        """
+        x_rows, out = self._layernorm("fused_layernorm", x, None, weight, bias, eps,
+                                      normed == "half", write_xnew=copy_x,
+                                      split=normed == "split", row_index=row_index)
+        return [x_rows, out]
+
+    def fused_add_layernorm_rows(self, x, sub, weight, bias, row_index, eps=1e-5):
+        """LayerNorm(x + sub)[row_index] in fp32, zero rows where row_index < 0.
+
+        Not in the reference's surface: the scatter back from packed rows to
+        the padded layout, fused with the model's last add+LN and the
+        reference's final masked_fill. The residual sum is not stored.
+        """
+        _, out = self._layernorm("fused_add_layernorm", x, sub, weight, bias, eps, False,
+                                 write_xnew=False, row_index=row_index)
+        return out
 
     def fused_add_layernorm(self, x, sub, weight, bias, eps=1e-5, normed_half=False):
         """[x + sub, LayerNorm(x + sub)] in one kernel."""
@@ -408,7 +453,17 @@ class Kernels:
     # -- attention (reference csrc/attention_dispatch.cuh:332-519) -------------------
 
     def fused_attention_forward(self, q, k, v, attn_mask=None, is_causal=False, scale=None,
-                                impl=0, out_layout=0, precision=0):
+                                impl=0, out_layout=0, precision=0, cu_seqlens=None,
+                                max_seqlen=None):
+        """softmax(q k^T * scale + mask) v (reference csrc/attention_dispatch.cuh:332-519).
+
+        q/k/v are [B, H, S, head_dim]. Beyond the reference's arguments:
+        with `cu_seqlens` (int32 [B + 1] on the device) they are packed
+        sequences instead, [rows, H, head_dim] with sequence b at rows
+        cu_seqlens[b] .. cu_seqlens[b + 1], `max_seqlen` (a host int) bounds
+        every sequence's length, there is no mask, and the output is
+        [rows, H * head_dim].
+        """
         import torch
 
         who = "fused_attention_forward"
@@ -422,43 +477,67 @@ class Kernels:
             raise RuntimeError(f"{who}: precision must be 0 (auto), 1 (fp32), 2 (tf32), 3 (fp16) or 4 (bf16)")
         if not (q.is_cuda and k.is_cuda and v.is_cuda):
             raise RuntimeError(f"{who}: q/k/v must be CUDA tensors")
-        if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
-            raise RuntimeError(f"{who}: q/k/v must be 4-D [B, H, S, head_dim]")
+        packed = cu_seqlens is not None
+        want_dim = 3 if packed else 4
+        if q.dim() != want_dim or k.dim() != want_dim or v.dim() != want_dim:
+            raise RuntimeError(f"{who}: q/k/v must be " + (
+                "3-D [rows, H, head_dim] with cu_seqlens" if packed else "4-D [B, H, S, head_dim]"))
         if q.shape != k.shape or q.shape != v.shape:
             raise RuntimeError(f"{who}: q/k/v must have identical shapes")
         if q.dtype != k.dtype or q.dtype != v.dtype:
             raise RuntimeError(f"{who}: q/k/v must share a dtype")
         code = _dtype_code(q)
-        B, H, S, hd = (int(s) for s in q.shape)
+        hd = int(q.shape[-1])
         if code is None:
             raise RuntimeError(f"{who}: impl={impl}, precision={precision} does not cover "
                                f"dtype={q.dtype}, head_dim={hd}: the MFMA kernel takes float16 "
                                f"or float32 tensors")
-        pass_strided = (q.stride(3) == 1 and k.stride(3) == 1 and v.stride(3) == 1
+        last = want_dim - 1
+        pass_strided = (q.stride(last) == 1 and k.stride(last) == 1 and v.stride(last) == 1
                         and q.stride() == k.stride() and q.stride() == v.stride())
         if not pass_strided:
             q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        if any((st * q.element_size()) % 16 for st in q.stride()[:3]):
+        if any((st * q.element_size()) % 16 for st in q.stride()[:last]):
             q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        strides = (ctypes.c_int64 * 3)(q.stride(0), q.stride(1), q.stride(2))
-        mask_ptr = None
-        ms = None
-        keep = None
-        if attn_mask is not None:
-            if attn_mask.dtype != torch.bool:
-                raise RuntimeError(f"{who}: attn_mask must be a bool tensor")
-            keep = attn_mask.contiguous().expand(B, H, S, S)
-            mask_ptr = keep.data_ptr()
-            ms = (ctypes.c_int64 * 4)(*keep.stride())
-        if out_layout == 1:
-            out = torch.empty((B, S, H * hd), dtype=q.dtype, device=q.device)
+        cu_ptr = None
+        if packed:
+            if attn_mask is not None:
+                raise RuntimeError(f"{who}: packed sequences (cu_seqlens) take no attn_mask")
+            if cu_seqlens.dtype != torch.int32 or cu_seqlens.dim() != 1 or not cu_seqlens.is_cuda:
+                raise RuntimeError(f"{who}: cu_seqlens must be a 1-D int32 CUDA tensor")
+            if max_seqlen is None or int(max_seqlen) < 0:
+                raise RuntimeError(f"{who}: max_seqlen (a host int) is required with cu_seqlens")
+            cu = cu_seqlens.contiguous()
+            cu_ptr = cu.data_ptr()
+            rows, H = int(q.shape[0]), int(q.shape[1])
+            B, S = cu.numel() - 1, int(max_seqlen)
+            strides = (ctypes.c_int64 * 3)(0, q.stride(1), q.stride(0))
+            out_layout = 1
+            out = torch.empty((rows, H * hd), dtype=q.dtype, device=q.device)
+            mask_ptr, ms, keep = None, None, None
+            if rows == 0:
+                B = 0
         else:
-            out = torch.empty((B, H, S, hd), dtype=q.dtype, device=q.device)
+            B, H, S = (int(s) for s in q.shape[:3])
+            strides = (ctypes.c_int64 * 3)(q.stride(0), q.stride(1), q.stride(2))
+            mask_ptr = None
+            ms = None
+            keep = None
+            if attn_mask is not None:
+                if attn_mask.dtype != torch.bool:
+                    raise RuntimeError(f"{who}: attn_mask must be a bool tensor")
+                keep = attn_mask.contiguous().expand(B, H, S, S)
+                mask_ptr = keep.data_ptr()
+                ms = (ctypes.c_int64 * 4)(*keep.stride())
+            if out_layout == 1:
+                out = torch.empty((B, S, H * hd), dtype=q.dtype, device=q.device)
+            else:
+                out = torch.empty((B, H, S, hd), dtype=q.dtype, device=q.device)
         rc = self._lib.dotl_attention_forward(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), code,
             strides, mask_ptr, ms, out.data_ptr(), code,
             out_layout, B, H, S, hd, 1 if is_causal else 0, float(scale), int(impl),
-            int(precision), self._stream(q.device))
+            int(precision), cu_ptr, self._stream(q.device))
         self._check(rc)
         if rc == DOTL_DECLINED:
             raise RuntimeError(self._err())

@@ -6,9 +6,10 @@ through the module (`config.CUDA_GRAPH = "off"`): a `from ... import` binds
 the value, not the setting. The thresholds below were re-derived for MI355X
 (256 CUs, 288 GB HBM3E) rather than carried over from the reference's card.
 
-Two knobs are new, both precision edges of this build:
+Three knobs are new in this build:
   QKV_PRECISION  arithmetic of the fused QKV projection
   GELU_FP16      whether linear_gelu stores its output as fp16 for ffn_out
+  ROW_PACKING    whether a padded batch runs on its valid rows only
 """
 
 # Attention backend. One legal value: the custom kernels, never a prebuilt
@@ -119,6 +120,13 @@ _GRAPH_MIN_FREE_BYTES = 512 << 20
 
 # Capture feeds the model its own data, from a local generator.
 _GRAPH_SEED = 20240827
+
+# Padded batches: "auto" runs the layer on the valid rows only (gathered by
+# the first LayerNorm, attention over packed sequences, scattered back by the
+# final add+LayerNorm with zero padded rows); "off" runs all B*S rows and
+# zeroes the padded ones with masked_fill, as the reference does. Same
+# outputs either way (bit-identical on prefix masks); see optimized/packing.py.
+ROW_PACKING = "auto"
 
 # Split the batch and retry when a forward runs out of memory.
 MICROBATCH_FALLBACK = True

@@ -28,9 +28,10 @@ class _GraphRunner:
     """One captured graph plus every buffer whose address it baked in."""
 
     __slots__ = ("graph", "stream", "static_x", "static_mask", "static_out", "needs_mask",
-                 "replays", "pinned", "__weakref__")
+                 "static_packing", "loaded_packing", "replays", "pinned", "__weakref__")
 
-    def __init__(self, graph, stream, static_x, static_mask, static_out, needs_mask, pinned):
+    def __init__(self, graph, stream, static_x, static_mask, static_out, needs_mask, pinned,
+                 static_packing=None, loaded_packing=None):
         self.graph = graph
         self.stream = stream
         self.static_x = static_x
@@ -38,13 +39,22 @@ class _GraphRunner:
         self.static_out = static_out
         self.needs_mask = needs_mask
         self.pinned = pinned
+        # Packed-row graphs read the row maps instead of the mask; the maps
+        # are reloaded only when the model hands in a different packing
+        # (a new mask object), not on every replay.
+        self.static_packing = static_packing
+        self.loaded_packing = loaded_packing
         self.replays = 0
 
-    def replay(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
+    def replay(self, x: torch.Tensor, mask: Optional[torch.Tensor],
+               packing=None) -> torch.Tensor:
         """Copy the inputs in, replay, return a clone of the output."""
         self.static_x.copy_(x)
         if self.needs_mask:
             self.static_mask.copy_(mask)
+        if self.static_packing is not None and packing is not self.loaded_packing:
+            self.static_packing.copy_(packing)
+            self.loaded_packing = packing
         self.graph.replay()
         self.replays += 1
         return self.static_out.clone()
@@ -60,13 +70,17 @@ class _GraphRunner:
         self.static_x = None
         self.static_mask = None
         self.static_out = None
+        self.static_packing = None
+        self.loaded_packing = None
         self.pinned = None
         torch.cuda.empty_cache()
 
 
-def _graph_key(x: torch.Tensor, use_mask: bool) -> Tuple:
-    """Everything a capture freezes: shape/dtype/device, mask mode and the knobs."""
+def _graph_key(x: torch.Tensor, use_mask: bool, packing=None) -> Tuple:
+    """Everything a capture freezes: shape/dtype/device, mask mode (and the
+    packed row count, which sizes the packed path's GEMMs) and the knobs."""
     return (tuple(x.shape), x.dtype, x.device.index, use_mask,
+            None if packing is None else packing.key(), config.ROW_PACKING,
             config.ATTENTION_IMPL, config.LINEAR_GELU, config.LINEAR_BIAS, config.LAYERNORM,
             config.QKV_FP16, config.NORMED_FP16, config.CP_ASYNC, config.ATTENTION_PRECISION,
             config.QKV_PRECISION, config.GELU_FP16)
@@ -147,12 +161,17 @@ def _graph_release(g) -> None:
 
 
 def _capture_graph(model, x: torch.Tensor, mask: Optional[torch.Tensor],
-                   use_mask: bool) -> Optional[_GraphRunner]:
-    """Capture model._forward_eager, or return None and leave the run eager."""
+                   use_mask: bool, packing=None) -> Optional[_GraphRunner]:
+    """Capture model._forward_eager, or return None and leave the run eager.
+
+    With `packing` the graph runs the packed-row path on static copies of the
+    row maps (loaded from `packing`) and never reads the mask.
+    """
     global _graph_noted, _graph_warned
     dev = x.device
     g = None
-    static_x = static_mask = static_out = ref = None
+    static_x = static_mask = static_out = ref = static_packing = None
+    needs_mask = use_mask and packing is None
     try:
         if _custom_kernels() is None:
             return None
@@ -166,13 +185,16 @@ def _capture_graph(model, x: torch.Tensor, mask: Optional[torch.Tensor],
         with torch.inference_mode(False):
             static_x = torch.empty(x.shape, dtype=x.dtype, device=dev)
             static_mask = (torch.empty(mask.shape, dtype=torch.bool, device=dev)
-                           if use_mask else None)
+                           if needs_mask else None)
             gen = torch.Generator(device=dev)
             gen.manual_seed(config._GRAPH_SEED)
             static_x.normal_(generator=gen)
-            if use_mask:
+            if needs_mask:
                 static_mask.fill_(True)
                 static_mask[:, static_mask.shape[1] // 2:] = False
+            if packing is not None:
+                static_packing = packing.empty_like()
+                static_packing.copy_(packing)
 
             with torch.no_grad():
                 # Warmup on the capture stream: builds the fused QKV weight and
@@ -181,16 +203,18 @@ def _capture_graph(model, x: torch.Tensor, mask: Optional[torch.Tensor],
                 side.wait_stream(torch.cuda.current_stream(dev))
                 with torch.cuda.stream(side):
                     for _ in range(config._GRAPH_WARMUP_ITERS):
-                        model._forward_eager(static_x, static_mask, use_mask)
+                        model._forward_eager(static_x, static_mask, use_mask, static_packing)
                 torch.cuda.current_stream(dev).wait_stream(side)
                 torch.cuda.synchronize(dev)
                 ptrs_before = _graph_cache_ptrs(model)
 
-                ref = model._forward_eager(static_x, static_mask, use_mask).clone()
+                ref = model._forward_eager(static_x, static_mask, use_mask,
+                                           static_packing).clone()
 
                 g = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g, stream=side):
-                    static_out = model._forward_eager(static_x, static_mask, use_mask)
+                    static_out = model._forward_eager(static_x, static_mask, use_mask,
+                                                      static_packing)
 
                 # Prove the graph computes what eager computes, on more than one
                 # replay (a replay-dependent node would show on the second).
@@ -227,20 +251,22 @@ def _capture_graph(model, x: torch.Tensor, mask: Optional[torch.Tensor],
             return None
 
         runner = _GraphRunner(graph=g, stream=side, static_x=static_x, static_mask=static_mask,
-                              static_out=static_out, needs_mask=use_mask,
-                              pinned=_graph_pinned_refs(model))
+                              static_out=static_out, needs_mask=needs_mask,
+                              pinned=_graph_pinned_refs(model), static_packing=static_packing,
+                              loaded_packing=packing)
         _graph_register(runner)
         if not _graph_noted:
             _graph_noted = True
             pool_mib = (torch.cuda.memory_reserved(dev) - reserved_before) / (1 << 20)
             print(f"[info] graph captured: shape={tuple(x.shape)} "
-                  f"{str(x.dtype).replace('torch.', '')} mask={'on' if use_mask else 'off'}, "
+                  f"{str(x.dtype).replace('torch.', '')} mask={'on' if use_mask else 'off'}"
+                  f"{' (packed rows)' if packing is not None else ''}, "
                   f"pool +{pool_mib:.1f} MiB, replay matches eager exactly")
         return runner
 
     except Exception as exc:  # noqa: BLE001
         _graph_release(g)
-        del static_x, static_mask, static_out, ref
+        del static_x, static_mask, static_out, ref, static_packing
         try:
             if torch.cuda.is_current_stream_capturing():
                 raise RuntimeError("stream is still capturing")

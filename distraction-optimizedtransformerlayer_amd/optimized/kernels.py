@@ -136,6 +136,53 @@ def _linear_bias_split(planes: torch.Tensor, weight: torch.Tensor, bias: torch.T
     return out.half() if out_half else out
 
 
+def _layernorm_pack(x: torch.Tensor, norm, packing) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(valid rows of x, LayerNorm of them): the gather into packed rows.
+
+    The normed rows take the form the QKV projection consumes: split fp16
+    planes for the fp16x3 projection, else fp16 or fp32 as _normed_wants_fp16
+    decides.
+    """
+    width = x.shape[-1]
+    if _normed_split_wanted():
+        kind = "split"
+    elif _normed_wants_fp16(packing.t_valid, width):
+        kind = "half"
+    else:
+        kind = "float"
+    kernels = _custom_kernels()
+    if kernels is not None:
+        x_rows, normed = kernels.fused_layernorm_rows(x, norm.weight, norm.bias, packing.idx,
+                                                      norm.eps, kind, True)
+        return x_rows, normed
+    fallback_counts["layernorm"] += 1
+    x_rows = x.reshape(-1, width).index_select(0, packing.idx.long())
+    out = F.layer_norm(x_rows, (width,), norm.weight, norm.bias, norm.eps)
+    if kind == "split":
+        return x_rows, _split_planes(out)
+    return x_rows, (out.half() if kind == "half" else out)
+
+
+def _add_layernorm_unpack(x: torch.Tensor, sub: torch.Tensor, norm, packing) -> torch.Tensor:
+    """LayerNorm(x + sub) of packed rows, returned as [B, S, D] with zero padded rows.
+
+    The model's last add+LN and the reference's final masked_fill in one
+    kernel; the residual sum is not stored.
+    """
+    width = x.shape[-1]
+    shape = (packing.batch, packing.seq_len, width)
+    kernels = _custom_kernels()
+    if kernels is not None:
+        out = kernels.fused_add_layernorm_rows(x, sub, norm.weight, norm.bias, packing.inv,
+                                               norm.eps)
+        return out.view(shape)
+    fallback_counts["add_layernorm"] += 1
+    y = F.layer_norm(x + sub, (width,), norm.weight, norm.bias, norm.eps)
+    out = torch.zeros(packing.batch * packing.seq_len, width, dtype=y.dtype, device=y.device)
+    out.index_copy_(0, packing.idx.long(), y)
+    return out.view(shape)
+
+
 def _layernorm(x: torch.Tensor, norm, out_half: bool = False) -> torch.Tensor:
     """LayerNorm(x) * w + b: the model's one norm with no residual before it."""
     if config.LAYERNORM != "off":
@@ -225,6 +272,31 @@ def _ffn_block(x, attn_out, norm1, ffn_in, ffn_out, norm2):
                                   ffn_in.bias, ffn_out.weight, ffn_out.bias, norm2.weight,
                                   norm2.bias, norm1.eps)
     return (out[0], out[1]) if out else None
+
+
+def _attention_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, packing,
+                      is_causal: bool, scale: float) -> torch.Tensor:
+    """Attention over packed sequences ([T_valid, H, hd] views) -> [T_valid, H*hd].
+
+    No mask: each sequence's rows are exactly its valid tokens. The grid is
+    sized by the padded length S (not the longest valid one), so a captured
+    graph depends on the packing's sizes only.
+    """
+    import kernel_ext
+
+    kernels = kernel_ext.get_kernels()
+    if kernels is None:
+        raise RuntimeError(
+            "the gfx950 extension (libdotl_hip.so) failed to load, and there is no "
+            "fallback: this project implements attention itself and will not substitute "
+            f"a prebuilt one. Cause: {kernel_ext.load_error()}")
+    _sync_attention_precision(kernels)
+    _sync_cp_async(kernels)
+    return kernels.fused_attention_forward(
+        q, k, v, None, is_causal, scale,
+        config._IMPL_CODE[config.ATTENTION_IMPL], config._OUT_LAYOUT_BSHD,
+        config._PRECISION_CODE[config.ATTENTION_PRECISION],
+        cu_seqlens=packing.cu, max_seqlen=packing.seq_len)
 
 
 def _attention_dispatch(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

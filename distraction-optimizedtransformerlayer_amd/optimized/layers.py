@@ -13,11 +13,11 @@ import torch
 import torch.nn as nn
 
 from . import config
-from .kernels import (_add_layernorm, _add_layernorm_split, _attention_dispatch,
-                      _attention_wants_fp16, _ffn_block, _gelu_input_wants_fp16,
-                      _gelu_output_wants_fp16, _layernorm, _layernorm_split, _linear_bias,
-                      _linear_bias_split, _linear_gelu, _normed_split_wanted,
-                      _normed_wants_fp16, _qkv_math_code)
+from .kernels import (_add_layernorm, _add_layernorm_split, _add_layernorm_unpack,
+                      _attention_dispatch, _attention_packed, _attention_wants_fp16,
+                      _ffn_block, _gelu_input_wants_fp16, _gelu_output_wants_fp16,
+                      _layernorm, _layernorm_split, _linear_bias, _linear_bias_split,
+                      _linear_gelu, _normed_split_wanted, _normed_wants_fp16, _qkv_math_code)
 from .util import _version_or_none
 
 
@@ -94,9 +94,18 @@ class MySelfAttention(nn.Module):
         return self._qkv_weight, self._qkv_bias
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,
-                causal: bool = False, mask_is_trivial: bool = False) -> torch.Tensor:
+                causal: bool = False, mask_is_trivial: bool = False,
+                packing=None) -> torch.Tensor:
         """`x` is [B, S, D], or [2, B, S, D] split fp16 planes of it (the form
-        a LayerNorm emits for the fp16x3 projection)."""
+        a LayerNorm emits for the fp16x3 projection).
+
+        With `packing` (an optimized.packing.RowPacking), `x` holds only the
+        valid rows, [T_valid, D] or planes [2, T_valid, D]; attention runs over
+        the packed sequences and the result is [T_valid, D], with no padded
+        rows to zero.
+        """
+        if packing is not None:
+            return self._forward_packed(x, causal, packing)
         split = x.dim() == 4
         batch, seq_len = (x.shape[1], x.shape[2]) if split else (x.shape[0], x.shape[1])
         qkv_w, qkv_b = self._get_qkv_weight()
@@ -123,6 +132,21 @@ class MySelfAttention(nn.Module):
             output = output.masked_fill(~valid_token_mask[..., None], 0)
         return output
 
+    def _forward_packed(self, x: torch.Tensor, causal: bool, packing) -> torch.Tensor:
+        split = x.dim() == 3
+        rows = packing.t_valid
+        qkv_w, qkv_b = self._get_qkv_weight()
+        want_half = (_attention_wants_fp16()
+                     and config._QKV_FP16_MIN_ROWS <= rows <= config._LINEAR_BIAS_MAX_ROWS)
+        if split:
+            qkv = _linear_bias_split(x, qkv_w, qkv_b, out_half=want_half)
+        else:
+            qkv = _linear_bias(x, qkv_w, qkv_b, out_half=want_half, math=_qkv_math_code())
+        # [T_valid, 3, H, hd] -> three strided [T_valid, H, hd] views.
+        q, k, v = qkv.view(rows, 3, self.num_heads, self.head_dim).unbind(1)
+        context = _attention_packed(q, k, v, packing, causal, self.scale)
+        return self.out_proj(context)
+
 
 class MyTransformerBlock(nn.Module):
     """BaselineTransformerBlock's submodule names (norm1, attention, norm2, ffn_in, ffn_out)."""
@@ -138,13 +162,22 @@ class MyTransformerBlock(nn.Module):
 
     def forward(self, x: torch.Tensor, normed: torch.Tensor, next_norm: "MyLayerNorm",
                 valid_token_mask: Optional[torch.Tensor] = None, mask_is_trivial: bool = False,
-                next_norm_is_output: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+                next_norm_is_output: bool = False,
+                packing=None) -> Tuple[Optional[torch.Tensor], torch.Tensor]:
         """Returns (residual stream, next_norm applied to it).
 
         `normed` is norm1(x), computed by whoever produced x; `next_norm` is
         the LayerNorm that consumes this block's output (the next block's
         norm1, or final_norm), so both residual adds fuse with a norm.
+
+        With `packing`, x and normed hold the valid rows only ([T_valid, D];
+        normed may be split planes) and so does the result, except when
+        next_norm is the model's output norm: that one is returned in the
+        padded [B, S, D] layout with zero padded rows, and the residual
+        stream, which nothing reads after it, is not materialised (None).
         """
+        if packing is not None:
+            return self._forward_packed(x, normed, next_norm, next_norm_is_output, packing)
         attn_out = self.attention(normed, valid_token_mask, self.causal, mask_is_trivial)
         use_mask = valid_token_mask is not None and not mask_is_trivial
 
@@ -169,6 +202,24 @@ class MyTransformerBlock(nn.Module):
         trailing_half = (not next_norm_is_output
                          and _normed_wants_fp16(rows, x.shape[-1]))
         return _add_layernorm(x, ffn_out, next_norm, normed_half=trailing_half)
+
+    def _forward_packed(self, x, normed, next_norm, next_norm_is_output, packing):
+        attn_out = self.attention(normed, None, self.causal, True, packing=packing)
+        if not next_norm_is_output:
+            fused = _ffn_block(x, attn_out, self.norm2, self.ffn_in, self.ffn_out, next_norm)
+            if fused is not None:
+                return fused
+        rows, width = packing.t_valid, x.shape[-1]
+        x, normed = _add_layernorm(x, attn_out, self.norm2,
+                                   normed_half=_gelu_input_wants_fp16(rows, width))
+        hidden = _linear_gelu(normed, self.ffn_in, out_half=_gelu_output_wants_fp16(rows))
+        ffn_out = self.ffn_out(hidden)
+        if next_norm_is_output:
+            return None, _add_layernorm_unpack(x, ffn_out, next_norm, packing)
+        if _normed_split_wanted():
+            return _add_layernorm_split(x, ffn_out, next_norm)
+        return _add_layernorm(x, ffn_out, next_norm,
+                              normed_half=_normed_wants_fp16(rows, width))
 
 
 def _final_norm(x: torch.Tensor, norm: "MyLayerNorm") -> torch.Tensor:

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DOTL_ABI_VERSION 1
+#define DOTL_ABI_VERSION 2
 
 #define DOTL_OK 0
 #define DOTL_DECLINED 1
@@ -87,18 +87,27 @@ int dotl_mfma_layout_probe(int32_t* out, void* stream);
  *
  *   x, sub      [rows, D] contiguous, dtype DOTL_F32. sub == NULL: plain LN.
  *   weight,bias [D] float32
- *   x_new       [rows, D] float32 output, x + sub (rounded to fp32); may be
- *               NULL to skip the store (required NULL when sub == NULL)
+ *   x_new       [rows, D] float32 output, x + sub (rounded to fp32), or x alone
+ *               when sub == NULL; may be NULL to skip the store
  *   normed      [rows, D] output of dtype normed_dtype (DOTL_F32; DOTL_F16, RNE
  *               narrowing; or DOTL_F16X2, [2][rows][D] split planes for the
  *               DOTL_MATH_FP16X3 GEMM), LayerNorm(x + sub) * weight + bias
+ *   row_index   optional (NULL) int32 [rows]: output row t reads input row
+ *               row_index[t] of x and sub ([in_rows, D] each), and an entry
+ *               outside [0, in_rows) writes zeros to every output of row t.
+ *               Without it, x and sub are [rows, D] and in_rows is ignored. Packs the valid rows of a padded batch
+ *               (gather) and returns them to the padded layout with zeroed
+ *               padding (scatter) -- the reference zeroes padded rows with
+ *               masked_fill (reference optimized/layers.py:247-252,
+ *               optimized/model.py:141-142); no reference counterpart of its own.
  *   Statistics: fp32, mean then the centred sum of squares (biased variance),
  *   eps inside the square root.
  *   D in [1, 8192]; rows >= 0.
  */
 int dotl_layernorm(const void* x, const void* sub, const float* weight, const float* bias,
-                   void* x_new, void* normed, int64_t rows, int64_t D, double eps,
-                   int dtype, int normed_dtype, void* stream);
+                   void* x_new, void* normed, const int32_t* row_index, int64_t in_rows,
+                   int64_t rows, int64_t D, double eps, int dtype, int normed_dtype,
+                   void* stream);
 
 /*
  * Weight preparation for dotl_linear: w_hi = fp16(w) (RNE) and, when w_lo is
@@ -153,6 +162,15 @@ int dotl_linear(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
  *   is_causal    key j > query i is excluded (combinable with mask)
  *   impl         0 auto, 1 scalar, 2 wmma (here: the MFMA kernel), 3 tile
  *   precision    0 auto, 1 fp32, 2 tf32, 3 fp16, 4 bf16
+ *   cu_seqlens   optional (NULL) int32 [B + 1], non-decreasing, cu[0] = 0:
+ *                packed sequences. Sequence b is rows [cu[b], cu[b+1]) of
+ *                q/k/v (row stride qkv_strides[2], head stride
+ *                qkv_strides[1]; qkv_strides[0] unused) and of out, which is
+ *                then [cu[B], H*head_dim] (out_layout must be 1, mask NULL).
+ *                S must be >= the longest sequence. This is the padded
+ *                batch with its padding removed: no reference counterpart of
+ *                its own (the reference masks padded keys,
+ *                reference csrc/attention_dispatch.cuh:404-450).
  *   A query row with no allowed key produces 0.
  *   Returns DOTL_DECLINED when no kernel covers (dtype, head_dim); the caller
  *   raises, as the reference does.
@@ -162,7 +180,7 @@ int dotl_attention_forward(const void* q, const void* k, const void* v, int dtyp
                            const int64_t* mask_strides, void* out, int out_dtype,
                            int out_layout, int B, int H, int S, int head_dim,
                            int is_causal, double scale, int impl, int precision,
-                           void* stream);
+                           const int32_t* cu_seqlens, void* stream);
 
 /*
  * Fused post-attention block (add+LN, Linear+GELU, Linear, add+LN).

@@ -42,7 +42,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_and_target(lib):
-    assert lib.dotl_abi_version() == 1
+    assert lib.dotl_abi_version() == 2
     assert lib.dotl_target() == b"gfx950"
 
 
@@ -69,7 +69,8 @@ def _attn(lib, **kw):
     return lib.dotl_attention_forward(None, None, None, args["dtype"], strides, None, None,
                                       None, args["dtype"], args["out_layout"], args["B"],
                                       args["H"], args["S"], args["hd"], args["causal"],
-                                      ctypes.c_double(0.125), args["impl"], args["prec"], None)
+                                      ctypes.c_double(0.125), args["impl"], args["prec"],
+                                      args.get("cu"), None)
 
 
 def test_attention_vocabulary_checks(lib):
@@ -85,15 +86,21 @@ def test_attention_vocabulary_checks(lib):
     assert _attn(lib, impl=1) == 1
     # an empty problem on the covered path launches nothing
     assert _attn(lib, S=0) == 0
+    # packed sequences write the packed layout: out_layout 0 is refused
+    cu = (ctypes.c_int32 * 2)(0, 4)
+    assert _attn(lib, S=4, out_layout=0, cu=ctypes.cast(cu, ctypes.c_void_p)) == -1
 
 
 def test_layernorm_checks(lib):
-    assert lib.dotl_layernorm(None, None, None, None, None, None, 4, 0, ctypes.c_double(1e-5),
-                              0, 0, None) == -1  # D = 0
-    assert lib.dotl_layernorm(None, None, None, None, None, None, 0, 64, ctypes.c_double(1e-5),
-                              0, 0, None) == 0  # no rows
-    assert lib.dotl_layernorm(None, None, None, None, None, None, 4, 64, ctypes.c_double(1e-5),
-                              1, 0, None) == 1  # fp16 input declined
+    def ln(rows, D, dtype=0, row_index=None, in_rows=0):
+        return lib.dotl_layernorm(None, None, None, None, None, None, row_index, in_rows, rows, D,
+                                  ctypes.c_double(1e-5), dtype, 0, None)
+
+    assert ln(4, 0) == -1        # D = 0
+    assert ln(0, 64) == 0        # no rows
+    assert ln(4, 64, dtype=1) == 1   # fp16 input declined
+    idx = (ctypes.c_int32 * 1)(0)
+    assert ln(1, 64, row_index=ctypes.cast(idx, ctypes.c_void_p), in_rows=-1) == -1
 
 
 def test_ffn_block_declines(lib):
