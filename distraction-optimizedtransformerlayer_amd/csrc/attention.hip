@@ -37,11 +37,13 @@
 //     by every wavefront from a ballot, so no barrier is needed;
 //   * all mask/causal/bounds tests are compiled into a slow path taken only
 //     by tiles that need it (boundary, diagonal, or masked tiles).
-#include "dotl_common.h"
+#include "attention_params.h"
 
 namespace dotl {
 
 int attention_fp16_default();
+int attention_cp_async_mode();
+void attention_pipeline(int* nw, int* ns);
 
 namespace {
 
@@ -70,22 +72,6 @@ __device__ __forceinline__ half8 load8(const typename Elem<IN_F32>::T* p) {
         return *reinterpret_cast<const half8*>(p);
     }
 }
-
-struct AttnParams {
-    const void* q;
-    const void* k;
-    const void* v;
-    int64_t sb, sh, ss;          // q/k/v strides (elements): batch, head, seq
-    const uint8_t* mask;         // nullable
-    int64_t mb, mh, mq, mk;      // mask strides (elements)
-    const int32_t* cu;           // nullable: sequence b is rows [cu[b], cu[b+1]) (packed rows)
-    void* out;
-    int out_layout;              // 0 [B,H,S,hd], 1 [B,S,H*hd]
-    int B, H, S;
-    int nqb;                     // query blocks per (b, h)
-    int causal;
-    float scale_log2;            // scale * log2(e)
-};
 
 template <int HD, int NW, bool IN_F32, bool OUT_F32>
 __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
@@ -379,10 +365,8 @@ void launch_attn(const AttnParams& p, hipStream_t stream) {
                        dim3(NW * 64), 0, stream, p);
 }
 
-// Wavefronts per workgroup: enough to cover short sequences without idle
-// waves, 4 otherwise. p.nqb must already be query_blocks(S).
-int waves_for(int S) { return S <= 32 ? 1 : (S <= 64 ? 2 : 4); }
-int query_blocks(int S) { return (S + 32 * waves_for(S) - 1) / (32 * waves_for(S)); }
+int waves_for(int S) { return attn_waves_for(S); }
+int query_blocks(int S) { return attn_query_blocks(S); }
 
 template <int HD, bool IN_F32, bool OUT_F32>
 void launch_nw(const AttnParams& p, hipStream_t stream) {
@@ -510,7 +494,14 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
     p.out_layout = out_layout;
     p.B = B; p.H = H; p.S = S;
     p.causal = is_causal ? 1 : 0;
-    p.nqb = query_blocks(S);
+    int nw = waves_for(S), ns = 0;
+    if (dtype == DOTL_F16 && attention_cp_async_mode() != 0) {
+        int fnw = 0, fns = 0;
+        attention_pipeline(&fnw, &fns);
+        if (fnw == 1 || fnw == 2 || fnw == 4) nw = fnw;
+        if (fns >= 1 && fns <= 4) ns = fns;
+    }
+    p.nqb = (S + 32 * nw - 1) / (32 * nw);
     DOTL_REQUIRE(static_cast<int64_t>(p.nqb) * B * H <= 0x7fffffff,
                  "fused_attention_forward: grid too large");
     p.scale_log2 = static_cast<float>(scale * 1.4426950408889634);
@@ -521,6 +512,11 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
     const bool out32 = out_dtype == DOTL_F32;
     if (in32) {
         launched = out32 ? launch_hd<true, true>(head_dim, p, st) : launch_hd<true, false>(head_dim, p, st);
+    } else if (attention_cp_async_mode() != 0) {
+        // fp16 q/k/v: K/V tiles streamed into LDS asynchronously (the
+        // reference's cp_async staging; mode 0 selects the register-staged
+        // kernel below).
+        launched = launch_attn_dma(p, head_dim, out32, nw, ns, st);
     } else {
         launched = out32 ? launch_hd<false, true>(head_dim, p, st) : launch_hd<false, false>(head_dim, p, st);
     }

@@ -1,0 +1,40 @@
+// Launch parameters shared by the two attention kernels (attention.hip:
+// register-staged, any input dtype; attention_dma.hip: LDS-DMA pipelined,
+// fp16 inputs).
+#pragma once
+
+#include "dotl_common.h"
+
+namespace dotl {
+
+struct AttnParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    int64_t sb, sh, ss;          // q/k/v strides (elements): batch, head, seq
+    const uint8_t* mask;         // nullable
+    int64_t mb, mh, mq, mk;      // mask strides (elements)
+    const int32_t* cu;           // nullable: sequence b is rows [cu[b], cu[b+1]) (packed rows)
+    void* out;
+    int out_layout;              // 0 [B,H,S,hd], 1 [B,S,H*hd]
+    int B, H, S;
+    int nqb;                     // query blocks per (b, h)
+    int causal;
+    float scale_log2;            // scale * log2(e)
+};
+
+// Wavefronts per workgroup (32 queries each) for a sequence length: enough
+// to cover short sequences without idle waves, 4 otherwise.
+inline int attn_waves_for(int S) { return S <= 32 ? 1 : (S <= 64 ? 2 : 4); }
+inline int attn_query_blocks(int S) {
+    const int bm = 32 * attn_waves_for(S);
+    return (S + bm - 1) / bm;
+}
+
+// The pipelined kernel for fp16 q/k/v with nw waves per workgroup (1, 2 or
+// 4; p.nqb must be the matching query-block count) and ns pipeline stages
+// (1 to 4, or 0 for the default); false when head_dim is not covered.
+bool launch_attn_dma(const AttnParams& p, int head_dim, bool out_f32, int nw, int ns,
+                     hipStream_t stream);
+
+}  // namespace dotl

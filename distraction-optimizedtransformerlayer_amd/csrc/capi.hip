@@ -10,6 +10,8 @@ namespace {
 thread_local std::string g_last_error;
 std::atomic<int> g_wmma_fp16{1};
 std::atomic<int> g_cp_async{2};
+std::atomic<int> g_attn_nw{0};
+std::atomic<int> g_attn_ns{0};
 }  // namespace
 
 void set_error(const std::string& msg) { g_last_error = msg; }
@@ -25,6 +27,11 @@ int check_launch(const char* who) {
 }
 
 int attention_fp16_default() { return g_wmma_fp16.load(std::memory_order_relaxed); }
+int attention_cp_async_mode() { return g_cp_async.load(std::memory_order_relaxed); }
+void attention_pipeline(int* nw, int* ns) {
+    *nw = g_attn_nw.load(std::memory_order_relaxed);
+    *ns = g_attn_ns.load(std::memory_order_relaxed);
+}
 
 namespace {
 
@@ -138,6 +145,10 @@ int dotl_lds_dma_probe(const int32_t* src, int32_t* out, void* stream) {
 void dotl_wmma_set_fp16(int on) { dotl::g_wmma_fp16.store(on ? 1 : 0); }
 int dotl_wmma_fp16(void) { return dotl::g_wmma_fp16.load(); }
 void dotl_wmma_set_cp_async(int mode) { dotl::g_cp_async.store(mode); }
+void dotl_attention_set_pipeline(int waves, int stages) {
+    dotl::g_attn_nw.store(waves);
+    dotl::g_attn_ns.store(stages);
+}
 int dotl_wmma_cp_async_mode(void) { return dotl::g_cp_async.load(); }
 
 }  // extern "C"

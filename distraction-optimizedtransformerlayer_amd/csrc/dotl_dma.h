@@ -1,0 +1,56 @@
+// HBM -> LDS streaming helpers shared by the pipelined kernels (GEMM,
+// attention): the LDS-DMA load, an explicit vector-memory wait, and the
+// barrier that does not drain the pipeline.
+#pragma once
+
+#include "dotl_common.h"
+
+namespace dotl {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier for a pipeline. __syncthreads() carries a release fence,
+// which would make every wave drain ALL its outstanding DMAs (vmcnt(0)) --
+// including the younger tiles that are meant to stay in flight. Here the
+// wave first waits (explicitly, before calling this) for the DMAs of the tile
+// about to be read, and the barrier only needs this wave's LDS reads of the
+// stage about to be refilled to be complete (lgkmcnt(0)). The memory clobber
+// keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void stage_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// One 16-byte-per-lane LDS-DMA load: lane l's 16 bytes at g land at
+// lds + 16 l (lds wave-uniform). Issued from inline assembly so the
+// compiler's wait-count bookkeeping does not see it: the compiler would
+// otherwise drain every outstanding DMA (vmcnt(0)) before any read of a stage
+// that still has one in flight, collapsing the pipeline. The kernel's own
+// wait_vmcnt calls order the reads instead. M0 (the LDS base register of the
+// instruction) is saved and restored around it.
+__device__ __forceinline__ void dma16(const void* g, const void* lds) {
+    // wave-uniform by contract; readfirstlane puts it in an SGPR where the
+    // compiler cannot prove the uniformity itself
+    const unsigned base = __builtin_amdgcn_readfirstlane(
+        static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_void_t*)(lds))));
+    unsigned saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %2, off\n\t"
+        "s_nop 0\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(base), "v"(g)
+        : "memory");
+}
+
+}  // namespace dotl

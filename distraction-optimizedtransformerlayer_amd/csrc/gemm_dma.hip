@@ -40,7 +40,7 @@
 //     from one row address per tile. The epilogue's cost matters here: with
 //     one workgroup per CU nothing overlaps it, and at the configs' short K
 //     (256-512) it was costing more than the MFMAs.
-#include "dotl_common.h"
+#include "dotl_dma.h"
 
 namespace dotl {
 
@@ -49,8 +49,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kXcds = 8;
 constexpr int kGroupM = 8;
-
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ void tile_of(int64_t id, int64_t nm, int64_t nn, int64_t& mt,
                                         int64_t& nt) {
@@ -64,25 +62,6 @@ __device__ __forceinline__ void tile_of(int64_t id, int64_t nm, int64_t nn, int6
     const int64_t r = id - group * in_group;
     mt = first_m + r % gsize;
     nt = r / gsize;
-}
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
-// vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at maximum).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// Workgroup barrier for the pipeline. __syncthreads() carries a release
-// fence, which would make every wave drain ALL its outstanding DMAs
-// (vmcnt(0)) -- including the younger tiles that are meant to stay in
-// flight. Here the wave first waits (explicitly, before calling this) for the
-// DMAs of the tile about to be read, and the barrier only needs this wave's
-// LDS reads of the stage about to be refilled to be complete (lgkmcnt(0)).
-// The memory clobber keeps the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void stage_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 template <int BM, int BN, int BK, int PASSES>
@@ -102,28 +81,6 @@ struct DmaLayout {
     static_assert(BM % ROWS_PER_ROUND == 0 && BN % ROWS_PER_ROUND == 0, "rows per round");
     __device__ __forceinline__ static int swz(int row) { return (row / SWZ_DIV) % CPR; }
 };
-
-// One 16-byte-per-lane LDS-DMA load: lane l's 16 bytes at g land at
-// lds + 16 l. Issued from inline assembly so the compiler's wait-count
-// bookkeeping does not see it: the compiler would otherwise drain every
-// outstanding DMA (vmcnt(0)) before any read of a stage that still has one in
-// flight, collapsing the pipeline. The kernel's own wait_vmcnt calls order
-// the reads instead. M0 (the LDS base register of the instruction) is saved
-// and restored around it.
-__device__ __forceinline__ void dma16(const void* g, const _Float16* lds) {
-    const unsigned base = static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_void_t*)(lds)));
-    unsigned saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %2, off\n\t"
-        "s_nop 0\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(base), "v"(g)
-        : "memory");
-}
 
 // Fill `ROWS` rows of a stage region from src (row pitch K halves), rows
 // past `nrows` clamped. One DMA instruction per wave per ROWS_PER_DMA rows.

@@ -55,6 +55,7 @@ EXPORTED_SYMBOLS = (
     "dotl_mfma_layout_probe", "dotl_layernorm", "dotl_weight_split", "dotl_linear",
     "dotl_attention_forward", "dotl_ffn_block", "dotl_wmma_set_fp16", "dotl_wmma_fp16",
     "dotl_wmma_set_cp_async", "dotl_wmma_cp_async_mode", "dotl_lds_dma_probe",
+    "dotl_attention_set_pipeline",
 )
 
 _kernels = None
@@ -115,6 +116,8 @@ def _declare(lib) -> None:
     lib.dotl_wmma_set_cp_async.restype = None
     lib.dotl_wmma_set_cp_async.argtypes = [i32]
     lib.dotl_wmma_cp_async_mode.restype = i32
+    lib.dotl_attention_set_pipeline.restype = None
+    lib.dotl_attention_set_pipeline.argtypes = [i32, i32]
 
 
 def load_library(path: Optional[str] = None):
@@ -573,6 +576,12 @@ class Kernels:
 
     def wmma_set_cp_async(self, mode: int) -> None:
         self._lib.dotl_wmma_set_cp_async(int(mode))
+
+    def attention_set_pipeline(self, waves: int = 0, stages: int = 0) -> None:
+        """Force the LDS-DMA attention kernel's waves per workgroup (1, 2, 4)
+        and pipeline stages (1-4); 0 restores the automatic choice.
+        A measurement knob; not in the reference's surface."""
+        self._lib.dotl_attention_set_pipeline(int(waves), int(stages))
 
     def wmma_cp_async_mode(self) -> int:
         return int(self._lib.dotl_wmma_cp_async_mode())

@@ -204,12 +204,20 @@ int dotl_lds_dma_probe(const int32_t* src, int32_t* out, void* stream);
 /* Process-wide knobs with the reference's names
  * (reference csrc/fused_attention.cu:234-339). wmma_set_fp16 selects the
  * arithmetic "auto" attention precision resolves to: fp16 (1) or the split
- * fp16x3 path (0). cp_async has no gfx950 meaning; it is accepted and
- * remembered so callers that push it keep working. */
+ * fp16x3 path (0). cp_async selects how fp16 K/V tiles reach LDS, as the
+ * reference's cp.async staging knob does: 0 register-staged (load to VGPRs,
+ * then write LDS), 1 or 2 (default) asynchronous LDS-DMA through a
+ * multi-stage pipeline. */
 void dotl_wmma_set_fp16(int on);
 int dotl_wmma_fp16(void);
 void dotl_wmma_set_cp_async(int mode);
 int dotl_wmma_cp_async_mode(void);
+
+/* Measurement knob of the LDS-DMA attention kernel, no reference
+ * counterpart: force its wavefronts per workgroup (1, 2 or 4; 0 = by
+ * sequence length) and pipeline stages (1 to 4; 0 = by head_dim and length).
+ * Process-wide, like the knobs above. */
+void dotl_attention_set_pipeline(int waves, int stages);
 
 #ifdef __cplusplus
 }
