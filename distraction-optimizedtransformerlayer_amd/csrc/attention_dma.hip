@@ -32,8 +32,10 @@
 //     exceeds it by more than 2^8 (log2 domain 8), so after the first tiles
 //     the O^T rescale is skipped; P then stays <= 256, exact to fp16's
 //     relative precision, and l and O^T absorb the scale in fp32;
-//   * causal: key tiles past the workgroup's last query are never fetched,
-//     and workgroups are numbered so the heaviest query blocks start first.
+//   * causal: key tiles past the workgroup's last query are never fetched;
+//     the heavy query blocks are numbered first (descending) and the light
+//     ones after them ascending, so co-resident workgroups pair heavy with
+//     light.
 #include "attention_params.h"
 #include "dotl_dma.h"
 
@@ -100,7 +102,15 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dma_kernel(AttnParams p) {
     const int id = blockIdx.x;
     int qb = id / bh_count;
     const int bh = id - qb * bh_count;
-    if (p.causal) qb = p.nqb - 1 - qb;
+    if (p.causal) {
+        // Causal work grows with the query block. The first half of the grid
+        // takes the heavy blocks in descending order and the second half the
+        // light ones ascending, so blocks id and id + grid/2 -- which the
+        // dispatcher places on the same CU when the whole grid is resident --
+        // sum to the same work.
+        const int half = (p.nqb + 1) / 2;
+        qb = qb < half ? p.nqb - 1 - qb : qb - half;
+    }
     const int b = bh / p.H;
     const int h = bh - b * p.H;
 
@@ -157,22 +167,38 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dma_kernel(AttnParams p) {
     };
 
     // This wave's share of tile kt's DMAs: instructions wave, wave + NW, ...;
-    // 0 .. NDMA-1 fill K rows, NDMA .. 2 NDMA-1 fill V rows. Keys past the
-    // sequence are clamped to its last row (finite data, masked later).
+    // 0 .. NDMA-1 fill K rows, NDMA .. 2 NDMA-1 fill V rows. Each lane's
+    // byte offset within a tile (row r, swizzled chunk) is fixed, so a full
+    // tile is addressed as a scalar base (the tile's first key) plus that
+    // offset. The last tile clamps keys past the sequence to its last row
+    // (finite data, masked later).
+    unsigned lane_off[L];
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+        const int i = wave + NW * j;
+        const bool is_v = i >= TL::NDMA;
+        const int r = (is_v ? i - TL::NDMA : i) * TL::RPD + lane / TL::CPR;
+        const int lc = (lane % TL::CPR) ^ (is_v ? TL::fv(r) : TL::fk(r));
+        lane_off[j] = static_cast<unsigned>((static_cast<int64_t>(r) * p.ss + lc * 8) * 2);
+    }
     auto issue = [&](int kt, _Float16* ks_, _Float16* vs_) __attribute__((always_inline)) {
         const int key0 = kt * kKB;
-        const int sub = lane / TL::CPR;
-        const int pc = lane % TL::CPR;
+        const bool full_tile = key0 + kKB <= S;
 #pragma unroll
         for (int j = 0; j < L; ++j) {
             const int i = wave + NW * j;
             const bool is_v = i >= TL::NDMA;
             const int ii = is_v ? i - TL::NDMA : i;
-            const int r = ii * TL::RPD + sub;
-            const int lc = pc ^ (is_v ? TL::fv(r) : TL::fk(r));
-            const int key = min(key0 + r, S - 1);
-            const _Float16* src = (is_v ? vbase : kbase) + static_cast<int64_t>(key) * p.ss + lc * 8;
-            dma16(src, (is_v ? vs_ : ks_) + ii * TL::RPD * HD);
+            _Float16* dst = (is_v ? vs_ : ks_) + ii * TL::RPD * HD;
+            if (full_tile) {
+                const _Float16* base = (is_v ? vbase : kbase) + static_cast<int64_t>(key0) * p.ss;
+                dma16_off(base, lane_off[j], dst);
+            } else {
+                const int r = ii * TL::RPD + lane / TL::CPR;
+                const int lc = (lane % TL::CPR) ^ (is_v ? TL::fv(r) : TL::fk(r));
+                const int key = min(key0 + r, S - 1);
+                dma16((is_v ? vbase : kbase) + static_cast<int64_t>(key) * p.ss + lc * 8, dst);
+            }
         }
     };
 
@@ -200,21 +226,30 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dma_kernel(AttnParams p) {
             }
         }
 
+        // Softmax in the log2 domain with c = scale * log2(e): the maximum is
+        // taken over the raw scores and scaled once, and each probability is
+        // exp2(fma(s, c, -m)). A non-positive c (possible only through the C
+        // ABI) scales the scores first and runs the same code with c = 1.
+        float c = p.scale_log2;
+        if (!(c > 0.f)) {
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s[t2][r] *= c;
+            c = 1.f;
+        }
         const bool full = key0 + kKB <= S;
         const bool diag = p.causal && key0 + kKB - 1 > q_w0;
-        const bool needs_test = !full || diag || has_mask;
-        uint64_t live = ~0ull;
-        if (key_only_mask) {
-            const int key = key0 + lane;
-            live = __ballot(key < S && mbase[static_cast<int64_t>(key) * p.mk] != 0);
-        }
-        float tmax = -INFINITY;
+        if (!full || diag || has_mask) {
+            uint64_t live = ~0ull;
+            if (key_only_mask) {
+                const int key = key0 + lane;
+                live = __ballot(key < S && mbase[static_cast<int64_t>(key) * p.mk] != 0);
+            }
 #pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) {
+            for (int t2 = 0; t2 < 2; ++t2) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float x = s[t2][r] * p.scale_log2;
-                if (needs_test) {
+                for (int r = 0; r < 16; ++r) {
                     const int kl = t2 * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
                     const int key = key0 + kl;
                     bool ok = key < S;
@@ -227,29 +262,37 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dma_kernel(AttnParams p) {
                                        static_cast<int64_t>(key) * p.mk] != 0;
                         }
                     }
-                    if (!ok) x = -INFINITY;
+                    if (!ok) s[t2][r] = -INFINITY;
                 }
-                s[t2][r] = x;
-                tmax = fmaxf(tmax, x);
             }
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[t2][r]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave)) * c;
         float corr = 1.f;
         if (tmax > m_run + kLazyTau) {
             corr = __builtin_amdgcn_exp2f(m_run - tmax);   // 0 while m_run is -inf
             m_run = tmax;
         }
-        const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+        const float neg_m = (m_run == -INFINITY) ? 0.f : -m_run;
 
+        // P in fp16 (the PV operand), and its row sum from those same fp16
+        // values, two at a time in fp32 (v_dot2_f32_f16 against 1).
+        const half2v one2 = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
         float lsum = 0.f;
         half8 pf[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float pv = __builtin_amdgcn_exp2f(s[t >> 1][8 * (t & 1) + e] - m_use);
-                lsum += pv;
-                pf[t][e] = to_half(pv);
+            for (int e = 0; e < 8; ++e)
+                pf[t][e] = to_half(__builtin_amdgcn_exp2f(fmaf(s[t >> 1][8 * (t & 1) + e], c, neg_m)));
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const half2v pr = {pf[t][e], pf[t][e + 1]};
+                lsum = __builtin_amdgcn_fdot2(pr, one2, lsum, false);
             }
         }
         l_run = l_run * corr + lsum;

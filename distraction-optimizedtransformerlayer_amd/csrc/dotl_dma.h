@@ -28,6 +28,16 @@ __device__ __forceinline__ void stage_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// LDS byte offset of a generic pointer into LDS: the low 32 bits of a flat
+// address in the LDS aperture. Taken directly rather than through an
+// address-space cast, whose null check this toolchain's backend rejects
+// (an SGPR aperture operand in a VALU compare) in some kernels. Wave-uniform
+// by contract; readfirstlane puts it in an SGPR where the compiler cannot
+// prove the uniformity itself.
+__device__ __forceinline__ unsigned lds_offset(const void* lds) {
+    return __builtin_amdgcn_readfirstlane(static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds)));
+}
+
 // One 16-byte-per-lane LDS-DMA load: lane l's 16 bytes at g land at
 // lds + 16 l (lds wave-uniform). Issued from inline assembly so the
 // compiler's wait-count bookkeeping does not see it: the compiler would
@@ -36,10 +46,7 @@ __device__ __forceinline__ void stage_barrier() {
 // wait_vmcnt calls order the reads instead. M0 (the LDS base register of the
 // instruction) is saved and restored around it.
 __device__ __forceinline__ void dma16(const void* g, const void* lds) {
-    // wave-uniform by contract; readfirstlane puts it in an SGPR where the
-    // compiler cannot prove the uniformity itself
-    const unsigned base = __builtin_amdgcn_readfirstlane(
-        static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_void_t*)(lds))));
+    const unsigned base = lds_offset(lds);
     unsigned saved;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
@@ -50,6 +57,23 @@ __device__ __forceinline__ void dma16(const void* g, const void* lds) {
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
         : "s"(base), "v"(g)
+        : "memory");
+}
+
+// The same load addressed as a wave-uniform 64-bit base (SGPRs) plus this
+// lane's 32-bit byte offset: no per-lane 64-bit address arithmetic.
+__device__ __forceinline__ void dma16_off(const void* base, unsigned offset, const void* lds) {
+    const unsigned lbase = lds_offset(lds);
+    unsigned saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %2, %3\n\t"
+        "s_nop 0\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lbase), "v"(offset), "s"(base)
         : "memory");
 }
 
