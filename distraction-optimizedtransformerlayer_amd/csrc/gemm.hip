@@ -36,7 +36,7 @@
 
 namespace dotl {
 
-int pick_dma_tile(int64_t M, int64_t N, int passes);
+int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes);
 bool launch_gemm_dma(const _Float16* A, const _Float16* Alo, const _Float16* W,
                      const _Float16* Wlo, const float* bias, void* C, int64_t M, int64_t N,
                      int64_t K, int passes, int act, bool out_f16, int tile, hipStream_t stream);
@@ -452,7 +452,7 @@ extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const v
     DOTL_REQUIRE(math != DOTL_MATH_FP16X3 || w_lo != nullptr,
                  "%s: the fp16x3 math needs the split weight residual", who);
     DOTL_REQUIRE(((M + 63) / 64) * ((N + 63) / 64) <= 0x7fffffff, "%s: too large", who);
-    DOTL_REQUIRE(tile == -1 || (tile >= 0 && tile <= 4) || (tile >= 100 && tile <= 104),
+    DOTL_REQUIRE(tile == -1 || (tile >= 0 && tile <= 8) || (tile >= 100 && tile <= 104),
                  "%s: unknown tile id %d", who, tile);
     if (M == 0 || N == 0) return DOTL_OK;
     DOTL_REQUIRE(x && w_hi && bias && out, "%s: null pointer", who);
@@ -468,7 +468,7 @@ extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const v
         const _Float16* xh = static_cast<const _Float16*>(x);
         const _Float16* xl = x_dtype == DOTL_F16X2 ? xh + M * K : nullptr;
         const int passes = !split ? 1 : (x_dtype == DOTL_F16X2 ? 3 : 2);
-        const int t = tile < 0 ? pick_dma_tile(M, N, passes) : tile;
+        const int t = tile < 0 ? pick_dma_tile(M, N, K, passes) : tile;
         if (launch_gemm_dma(xh, xl, static_cast<const _Float16*>(w_hi),
                             static_cast<const _Float16*>(w_lo), bias, out, M, N, K, passes, act,
                             of16, t, as_stream(stream))) {
@@ -481,7 +481,7 @@ extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const v
     GemmArgs g{x, static_cast<const _Float16*>(w_hi), static_cast<const _Float16*>(w_lo), bias,
                out, M, N, K, as_stream(stream)};
     const bool a_f32 = x_dtype == DOTL_F32;
-    const int t = tile < 0 ? pick_tile(M, N, a_f32, split) : (tile % 100);
+    const int t = (tile < 0 || tile % 100 > 4) ? pick_tile(M, N, a_f32, split) : (tile % 100);
     bool ok;
     if (split) {
         ok = a_f32 ? launch_epilogue<true, true>(g, t, act, of16)

@@ -391,22 +391,49 @@ bool dispatch_tile(const DmaArgs& a, int tile) {
             else if constexpr (PASSES == 2) launch_dma<128, 64, 32, 7, PASSES, ACT, OUT_F16>(a);
             else launch_dma<128, 64, 32, 6, PASSES, ACT, OUT_F16>(a);
             return true;
+        // Shallow pipelines whose LDS (<= 72 KiB) lets two workgroups share a
+        // CU, i.e. two waves per SIMD, the co-resident one hiding latency.
+        case 5:
+            if constexpr (PASSES == 1) launch_dma<128, 128, 32, 4, PASSES, ACT, OUT_F16>(a);
+            else if constexpr (PASSES == 2) launch_dma<128, 128, 32, 3, PASSES, ACT, OUT_F16>(a);
+            else launch_dma<128, 128, 32, 2, PASSES, ACT, OUT_F16>(a);
+            return true;
+        case 6:
+            if constexpr (PASSES == 1) { launch_dma<256, 128, 32, 3, PASSES, ACT, OUT_F16>(a); return true; }
+            return false;
+        case 7:
+            if constexpr (PASSES == 1) launch_dma<128, 64, 32, 4, PASSES, ACT, OUT_F16>(a);
+            else launch_dma<128, 64, 32, 3, PASSES, ACT, OUT_F16>(a);
+            return true;
+        case 8:
+            launch_dma<64, 64, 32, 4, PASSES, ACT, OUT_F16>(a);
+            return true;
     }
     return false;
 }
 
 }  // namespace
 
-// Largest tile allowed for this arithmetic that still gives about one
-// workgroup per CU (256 CUs); else the one with the most workgroups.
-int pick_dma_tile(int64_t M, int64_t N, int passes) {
+// Tile choice, from sweeps of every GEMM of the five layer configs on MI355X:
+//   * one pass: 256x256 (deep pipeline, one workgroup per CU) once it gives a
+//     workgroup per CU; below that the shallow-pipeline tiles, two or more
+//     workgroups per CU, the largest that still fills the CUs;
+//   * split (fp16x3) passes: the deep 128x128 pipeline for K >= 1024; for
+//     short K (256-512, a handful of K tiles) the shallow 128x128 when there
+//     are plenty of tiles, else 128x64.
+int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     const int64_t fill = 240;
-    if (passes == 1 && tiles(256, 256) >= fill) return 3;
-    if (passes == 1 && tiles(256, 128) >= fill) return 1;
-    if (tiles(128, 128) >= fill) return 0;
-    if (tiles(128, 64) >= fill) return 4;
-    return 2;
+    if (passes == 1) {
+        if (tiles(256, 256) >= fill) return 3;
+        if (tiles(128, 128) >= fill) return 5;
+        if (tiles(128, 64) >= fill) return 7;
+        return 8;
+    }
+    if (K >= 1024 && tiles(128, 128) >= fill) return 0;
+    if (tiles(128, 128) >= 4 * fill) return 5;
+    if (tiles(128, 64) >= fill) return 7;
+    return 8;
 }
 
 bool launch_gemm_dma(const _Float16* A, const _Float16* Alo, const _Float16* W,

@@ -134,8 +134,10 @@ int dotl_weight_split(const float* w, void* w_hi, void* w_lo, int64_t n, void* s
  *             fp16, so with it the split path runs two passes: x*hi + x*lo;
  *             a DOTL_F16X2 x runs three: + lo(x)*hi(W))
  *   tile      -1 auto; otherwise a tile id (0: 128x128, 1: 256x128 [one
- *             pass], 2: 64x64, 3: 256x256 [one pass], 4: 128x64); 100 + id
- *             forces the register-staged kernel (for measurement)
+ *             pass], 2: 64x64, 3: 256x256 [one pass], 4: 128x64; 5-8: 128x128,
+ *             256x128 [one pass], 128x64, 64x64 with shallower pipelines that
+ *             fit two workgroups per CU); 100 + id (id <= 4) forces the
+ *             register-staged kernel (for measurement)
  *   fp16 / split-fp16 x with K % 64 == 0 runs the LDS-DMA pipelined kernel;
  *   anything else the register-staged one. Declines when K % 8 != 0, or a
  *   DOTL_F16X2 x with K % 64 != 0.
