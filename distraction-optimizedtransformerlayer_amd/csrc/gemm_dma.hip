@@ -415,9 +415,9 @@ bool dispatch_tile(const DmaArgs& a, int tile) {
 }  // namespace
 
 // Tile choice, from sweeps of every GEMM of the five layer configs on MI355X:
-//   * one pass: 256x256 (deep pipeline, one workgroup per CU) once it gives a
-//     workgroup per CU; below that the shallow-pipeline tiles, two or more
-//     workgroups per CU, the largest that still fills the CUs;
+//   * one pass: 256x256 (deep pipeline, one workgroup per CU) for K >= 2048
+//     once it gives a workgroup per CU; otherwise the shallow-pipeline tiles,
+//     two or more workgroups per CU, the largest that still fills the CUs;
 //   * split (fp16x3) passes: the deep 128x128 pipeline for K >= 1024; for
 //     short K (256-512, a handful of K tiles) the shallow 128x128 when there
 //     are plenty of tiles, else 128x64.
@@ -425,7 +425,7 @@ int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     const int64_t fill = 240;
     if (passes == 1) {
-        if (tiles(256, 256) >= fill) return 3;
+        if (K >= 2048 && tiles(256, 256) >= fill) return 3;
         if (tiles(128, 128) >= fill) return 5;
         if (tiles(128, 64) >= fill) return 7;
         return 8;
