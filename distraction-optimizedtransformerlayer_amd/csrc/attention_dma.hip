@@ -418,6 +418,166 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_dma_kernel(AttnParams p) {
     }
 }
 
+
+// Sequences of at most 32 keys (the mass-batch case: 16-token sequences,
+// thousands of them). One wavefront per (sequence, head) pair, four
+// independent pairs per workgroup and no barriers: K fragments are loaded
+// straight from HBM in MFMA layout (like Q), V goes by LDS-DMA into a
+// wave-private 32-row tile read back transposed as in the main kernel, and
+// the score tile is a single 32x32 accumulator (keys x queries).
+template <int HD, bool OUT_F32>
+__global__ __launch_bounds__(256) void attn_short_kernel(AttnParams p) {
+    using TL = AttnTile<HD>;
+    constexpr int KS = HD / 16;
+    constexpr int HT = HD / 32;
+    constexpr int ROWS = 32;
+    constexpr int SZ = ROWS * HD;                 // halves of V per wave
+    constexpr int ND = SZ * 2 / 1024;             // DMA instructions per wave
+    __shared__ __attribute__((aligned(1024))) _Float16 vsh[4 * SZ];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lr = lane & 31;
+    const int lg = lane >> 5;
+    const int pair = blockIdx.x * 4 + wave;
+    if (pair >= p.B * p.H) return;   // wave-uniform; this kernel has no barrier
+    const int b = pair / p.H;
+    const int h = pair - b * p.H;
+
+    int S = p.S;
+    int64_t seq_off = static_cast<int64_t>(b) * p.sb;
+    int64_t row0 = 0;
+    if (p.cu != nullptr) {
+        row0 = p.cu[b];
+        S = min(p.cu[b + 1] - static_cast<int>(row0), p.S);
+        seq_off = row0 * p.ss;
+    }
+    if (S <= 0) return;
+
+    const _Float16* qbase = static_cast<const _Float16*>(p.q) + seq_off + h * p.sh;
+    const _Float16* kbase = static_cast<const _Float16*>(p.k) + seq_off + h * p.sh;
+    const _Float16* vbase = static_cast<const _Float16*>(p.v) + seq_off + h * p.sh;
+    _Float16* vs = vsh + wave * SZ;
+
+    // V rows 0..31 (keys past the sequence clamped to its last row).
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+        const int r = j * TL::RPD + lane / TL::CPR;
+        const int lc = (lane % TL::CPR) ^ TL::fv(r);
+        const int key = min(r, S - 1);
+        dma16(vbase + static_cast<int64_t>(key) * p.ss + lc * 8, vs + j * TL::RPD * HD);
+    }
+
+    const int my_q = lr;
+    half8 qf[KS], kf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        qf[ks] = half8{};
+        kf[ks] = half8{};
+        if (my_q < S) {
+            qf[ks] = *reinterpret_cast<const half8*>(qbase + static_cast<int64_t>(my_q) * p.ss + ks * 16 + lg * 8);
+            kf[ks] = *reinterpret_cast<const half8*>(kbase + static_cast<int64_t>(my_q) * p.ss + ks * 16 + lg * 8);
+        }
+    }
+    floatx16 s = {};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks], qf[ks], s, 0, 0, 0);
+
+    float c = p.scale_log2;
+    if (!(c > 0.f)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] *= c;
+        c = 1.f;
+    }
+    const bool has_mask = p.mask != nullptr;
+    const uint8_t* mbase = has_mask ? p.mask + b * p.mb + h * p.mh : nullptr;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int key = 8 * (r >> 2) + 4 * lg + (r & 3);
+        bool ok = key < S;
+        if (p.causal) ok = ok && key <= my_q;
+        if (has_mask && ok && my_q < S)
+            ok = mbase[static_cast<int64_t>(my_q) * p.mq + static_cast<int64_t>(key) * p.mk] != 0;
+        if (!ok) s[r] = -INFINITY;
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave)) * c;
+    const float neg_m = (tmax == -INFINITY) ? 0.f : -tmax;
+    const half2v one2 = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
+    float lsum = 0.f;
+    half8 pf[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pf[t][e] = to_half(__builtin_amdgcn_exp2f(fmaf(s[8 * t + e], c, neg_m)));
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const half2v pr = {pf[t][e], pf[t][e + 1]};
+            lsum = __builtin_amdgcn_fdot2(pr, one2, lsum, false);
+        }
+    }
+    const float l_tot = lsum + __shfl_xor(lsum, 32, kWave);
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+
+    wait_vmcnt<0>();   // this wave's V tile has landed (only this wave reads it)
+    floatx16 o[HT];
+#pragma unroll
+    for (int j = 0; j < HT; ++j) o[j] = floatx16{};
+    const int hsel = (lane >> 4) & 1;
+    const int trow = (lane & 15) >> 2;
+    const int tchunk = 2 * hsel + ((lane & 3) >> 1);
+    const int thalf = 4 * (lane & 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int ra = 16 * t + 4 * lg + trow;
+        const int rb = ra + 8;
+#pragma unroll
+        for (int j = 0; j < HT; ++j) {
+            const int cc = 4 * j + tchunk;
+            const half4 a4 = lds_read_tr(vs + ra * HD + ((cc ^ TL::fv(ra)) * 8) + thalf);
+            const half4 b4 = lds_read_tr(vs + rb * HD + ((cc ^ TL::fv(rb)) * 8) + thalf);
+            const half8 vf = __builtin_shufflevector(a4, b4, 0, 1, 2, 3, 4, 5, 6, 7);
+            o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], o[j], 0, 0, 0);
+        }
+    }
+    if (my_q < S) {
+        const int64_t obase =
+            p.cu != nullptr
+                ? ((row0 + my_q) * p.H + h) * HD
+                : (p.out_layout == 1
+                       ? ((static_cast<int64_t>(b) * S + my_q) * p.H + h) * HD
+                       : ((static_cast<int64_t>(b) * p.H + h) * S + my_q) * HD);
+#pragma unroll
+        for (int j = 0; j < HT; ++j) {
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const int d = 32 * j + 8 * rb + 4 * lg;
+                if constexpr (OUT_F32) {
+                    const float4 w4 = make_float4(o[j][4 * rb] * inv, o[j][4 * rb + 1] * inv,
+                                                  o[j][4 * rb + 2] * inv, o[j][4 * rb + 3] * inv);
+                    *reinterpret_cast<float4*>(static_cast<float*>(p.out) + obase + d) = w4;
+                } else {
+                    half4 w4;
+                    w4[0] = to_half(o[j][4 * rb] * inv);
+                    w4[1] = to_half(o[j][4 * rb + 1] * inv);
+                    w4[2] = to_half(o[j][4 * rb + 2] * inv);
+                    w4[3] = to_half(o[j][4 * rb + 3] * inv);
+                    *reinterpret_cast<half4*>(static_cast<_Float16*>(p.out) + obase + d) = w4;
+                }
+            }
+        }
+    }
+}
+
+template <int HD, bool OUT_F32>
+void launch_short(const AttnParams& p, hipStream_t stream) {
+    const int64_t blocks = (static_cast<int64_t>(p.B) * p.H + 3) / 4;
+    hipLaunchKernelGGL((attn_short_kernel<HD, OUT_F32>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(256), 0, stream, p);
+}
+
 template <int HD, int NW, int NS, bool OUT_F32>
 void launch_one(const AttnParams& p, hipStream_t stream) {
     const int64_t blocks = static_cast<int64_t>(p.nqb) * p.B * p.H;
@@ -467,6 +627,14 @@ void launch_ns(const AttnParams& p, int nw, int ns, hipStream_t stream) {
 
 bool launch_attn_dma(const AttnParams& p, int head_dim, bool out_f32, int nw, int ns,
                      hipStream_t stream) {
+    if (p.S <= 32 && nw == attn_waves_for(p.S) && ns == 0) {
+        switch (head_dim) {
+            case 32: out_f32 ? launch_short<32, true>(p, stream) : launch_short<32, false>(p, stream); return true;
+            case 64: out_f32 ? launch_short<64, true>(p, stream) : launch_short<64, false>(p, stream); return true;
+            case 128: out_f32 ? launch_short<128, true>(p, stream) : launch_short<128, false>(p, stream); return true;
+            default: return false;
+        }
+    }
     switch (head_dim) {
         case 32: out_f32 ? launch_ns<32, true>(p, nw, ns, stream) : launch_ns<32, false>(p, nw, ns, stream); return true;
         case 64: out_f32 ? launch_ns<64, true>(p, nw, ns, stream) : launch_ns<64, false>(p, nw, ns, stream); return true;

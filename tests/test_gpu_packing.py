@@ -208,3 +208,38 @@ def test_packed_graph_reloads_maps_for_a_new_mask(kernels):
         assert not torch.equal(e1, e2)
     finally:
         ocfg.ROW_PACKING, ocfg.CUDA_GRAPH = prev
+
+
+@pytest.mark.parametrize("S", [1, 5, 16, 32])
+@pytest.mark.parametrize("hd", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_short_sequence_kernel_equals_tiled(kernels, S, hd, causal):
+    """Sequences of <= 32 keys take the one-wave-per-(sequence, head) kernel;
+    it must agree with the tiled kernel (forced through the pipeline knob)
+    to fp16 rounding of the output, packed and padded."""
+    B, H = 7, 3
+    torch.manual_seed(S * 100 + hd)
+    mask = _prefix_mask(B, S, S + hd, lo=1)
+    pk = build_packing(mask)
+    qkv = torch.randn(B, S, 3, H, hd, device=DEV).half()
+    q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+    pq, pk_, pv = qkv.reshape(B * S, 3, H, hd).index_select(0, pk.idx.long()).unbind(1)
+    scale = hd ** -0.5
+    outs = []
+    for forced in (False, True):
+        kernels.attention_set_pipeline(0, 1 if forced else 0)
+        try:
+            dense = kernels.fused_attention_forward(q, k, v, mask[:, None, None, :], causal,
+                                                    scale, 0, 1, 0)
+            packed = kernels.fused_attention_forward(pq, pk_, pv, None, causal, scale, 0, 1, 0,
+                                                     cu_seqlens=pk.cu, max_seqlen=S)
+            torch.cuda.synchronize()
+        finally:
+            kernels.attention_set_pipeline(0, 0)
+        outs.append((dense.float(), packed.float()))
+    (d0, p0), (d1, p1) = outs
+    ulp = 2.0 ** -10
+    assert (d0 - d1).abs().max().item() <= ulp * max(1.0, d1.abs().max().item())
+    assert (p0 - p1).abs().max().item() <= ulp * max(1.0, p1.abs().max().item())
+    # and packed equals the padded kernel on the valid rows, bit for bit
+    assert torch.equal(p0, d0.reshape(B * S, H * hd).index_select(0, pk.idx.long()))
