@@ -392,13 +392,15 @@ def run_config(name, steps, warmup, graph, with_kernels=True):
     x_np, mask_np, params = make_case(cfg)
     tcfg = TransformerConfig(cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads,
                              cfg.ffn_dim, 1, cfg.causal)
-    ocfg.CUDA_GRAPH = graph
     model = build_model(tcfg, params)
     x, mask = to_device(x_np, mask_np)
-    ms = time_layer(model, x, mask, steps, warmup)
+    # Eager first: a model replays a graph it has captured whatever the knob
+    # says later (as the reference's does), so the eager figure is taken
+    # before any capture.
     ocfg.CUDA_GRAPH = "off"
     ms_eager = time_layer(model, x, mask, max(5, steps // 2), 2)
     ocfg.CUDA_GRAPH = graph
+    ms = time_layer(model, x, mask, steps, warmup)
     L = lengths_of(mask_np, cfg, cfg.batch_size)
     flops = gemm_flops(cfg) + attention_useful_flops(cfg, L)
     res = dict(config=cfg, model=model, x=x, mask=mask, x_np=x_np, mask_np=mask_np,

@@ -58,24 +58,58 @@ struct Elem<false> { using T = _Float16; };
 template <>
 struct Elem<true> { using T = float; };
 
-// Load 8 consecutive head-dim elements as fp16 (narrowing fp32 with RNE).
-template <bool IN_F32>
-__device__ __forceinline__ half8 load8(const typename Elem<IN_F32>::T* p) {
+// MFMA operand type: fp16, or bf16 (fp32 tensors with precision=bf16).
+template <bool BF16>
+struct Ops;
+template <>
+struct Ops<false> {
+    using E = _Float16;
+    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+    typedef _Float16 v4 __attribute__((ext_vector_type(4)));
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    __device__ __forceinline__ static floatx16 mma(v8 a, v8 b, floatx16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct Ops<true> {
+    using E = __bf16;
+    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+    typedef __bf16 v4 __attribute__((ext_vector_type(4)));
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    __device__ __forceinline__ static floatx16 mma(v8 a, v8 b, floatx16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+// Load 8 consecutive head-dim elements as the operand type (narrowing fp32
+// with round-to-nearest-even).
+template <bool IN_F32, bool BF16>
+__device__ __forceinline__ typename Ops<BF16>::v8 load8(const typename Elem<IN_F32>::T* p) {
+    using O = Ops<BF16>;
     if constexpr (IN_F32) {
         const float4 a = *reinterpret_cast<const float4*>(p);
         const float4 b = *reinterpret_cast<const float4*>(p + 4);
-        half8 h;
-        h[0] = to_half(a.x); h[1] = to_half(a.y); h[2] = to_half(a.z); h[3] = to_half(a.w);
-        h[4] = to_half(b.x); h[5] = to_half(b.y); h[6] = to_half(b.z); h[7] = to_half(b.w);
+        typename O::v8 h;
+        h[0] = static_cast<typename O::E>(a.x); h[1] = static_cast<typename O::E>(a.y);
+        h[2] = static_cast<typename O::E>(a.z); h[3] = static_cast<typename O::E>(a.w);
+        h[4] = static_cast<typename O::E>(b.x); h[5] = static_cast<typename O::E>(b.y);
+        h[6] = static_cast<typename O::E>(b.z); h[7] = static_cast<typename O::E>(b.w);
         return h;
     } else {
+        static_assert(!BF16, "fp16 tensors contract in fp16");
         return *reinterpret_cast<const half8*>(p);
     }
 }
 
-template <int HD, int NW, bool IN_F32, bool OUT_F32>
+template <int HD, int NW, bool IN_F32, bool OUT_F32, bool BF16>
 __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
     using T = typename Elem<IN_F32>::T;
+    using O = Ops<BF16>;
+    using E = typename O::E;
+    using v8 = typename O::v8;
+    using v4 = typename O::v4;
+    using v2 = typename O::v2;
     constexpr int NT = NW * 64;
     constexpr int BM = NW * 32;
     constexpr int KS = HD / 16;          // k-steps of the score product
@@ -83,8 +117,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
     constexpr int LDK = HD + kKPad;      // K row pitch (halves)
     constexpr int LDV = kBN + kVPad;     // V^T row pitch (halves)
 
-    __shared__ __attribute__((aligned(16))) _Float16 sK[kBN * LDK];
-    __shared__ __attribute__((aligned(16))) _Float16 sVt[HD * LDV];
+    __shared__ __attribute__((aligned(16))) E sK[kBN * LDK];
+    __shared__ __attribute__((aligned(16))) E sVt[HD * LDV];
     __shared__ uint8_t sMask[kBN];
 
     const int lane = threadIdx.x & 63;
@@ -124,11 +158,11 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
     const T* vbase = static_cast<const T*>(p.v) + seq_off + h * p.sh;
 
     // Q^T fragments for the whole key loop: lane supplies Q[my_q][ks*16 + lg*8 .. +8].
-    half8 qf[KS];
+    v8 qf[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-        qf[ks] = half8{};
-        if (my_q < S) qf[ks] = load8<IN_F32>(qbase + static_cast<int64_t>(my_q) * p.ss + ks * 16 + lg * 8);
+        qf[ks] = v8{};
+        if (my_q < S) qf[ks] = load8<IN_F32, BF16>(qbase + static_cast<int64_t>(my_q) * p.ss + ks * 16 + lg * 8);
     }
 
     const bool has_mask = p.mask != nullptr;
@@ -154,8 +188,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
     // V: items are (key pair, 8-wide hd chunk): 32 * HD/8 of them.
     constexpr int VIT = 32 * HD / 8;
     constexpr int VPER = (VIT + NT - 1) / NT;
-    half8 rk[KPER];
-    half8 rv0[VPER], rv1[VPER];
+    v8 rk[KPER];
+    v8 rv0[VPER], rv1[VPER];
     uint8_t rm = 0;
 
     auto fetch = [&](int kt) {
@@ -165,21 +199,21 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
             const int c = threadIdx.x + i * NT;
             const int row = c / (HD / 8);
             const int col = (c % (HD / 8)) * 8;
-            rk[i] = half8{};
+            rk[i] = v8{};
             if (c < KCH && key0 + row < S)
-                rk[i] = load8<IN_F32>(kbase + static_cast<int64_t>(key0 + row) * p.ss + col);
+                rk[i] = load8<IN_F32, BF16>(kbase + static_cast<int64_t>(key0 + row) * p.ss + col);
         }
 #pragma unroll
         for (int i = 0; i < VPER; ++i) {
             const int it = threadIdx.x + i * NT;
             const int kp = it & 31;          // key pair
             const int ch = it >> 5;          // hd chunk
-            rv0[i] = half8{};
-            rv1[i] = half8{};
+            rv0[i] = v8{};
+            rv1[i] = v8{};
             if (it < VIT) {
                 const int k0 = key0 + 2 * kp;
-                if (k0 < S) rv0[i] = load8<IN_F32>(vbase + static_cast<int64_t>(k0) * p.ss + ch * 8);
-                if (k0 + 1 < S) rv1[i] = load8<IN_F32>(vbase + static_cast<int64_t>(k0 + 1) * p.ss + ch * 8);
+                if (k0 < S) rv0[i] = load8<IN_F32, BF16>(vbase + static_cast<int64_t>(k0) * p.ss + ch * 8);
+                if (k0 + 1 < S) rv1[i] = load8<IN_F32, BF16>(vbase + static_cast<int64_t>(k0 + 1) * p.ss + ch * 8);
             }
         }
         if (key_only_mask && threadIdx.x < kBN) {
@@ -195,7 +229,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
             if (c < KCH) {
                 const int row = c / (HD / 8);
                 const int col = (c % (HD / 8)) * 8;
-                *reinterpret_cast<half8*>(sK + row * LDK + col) = rk[i];
+                *reinterpret_cast<v8*>(sK + row * LDK + col) = rk[i];
             }
         }
 #pragma unroll
@@ -206,10 +240,10 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
                 const int ch = it >> 5;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    half2v pair;
+                    v2 pair;
                     pair[0] = rv0[i][e];
                     pair[1] = rv1[i][e];
-                    *reinterpret_cast<half2v*>(sVt + (ch * 8 + e) * LDV + 2 * kp) = pair;
+                    *reinterpret_cast<v2*>(sVt + (ch * 8 + e) * LDV + 2 * kp) = pair;
                 }
             }
         }
@@ -247,8 +281,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
             for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
                 for (int t2 = 0; t2 < 2; ++t2) {
-                    const half8 kf = *reinterpret_cast<const half8*>(sK + (t2 * 32 + lr) * LDK + ks * 16 + lg * 8);
-                    s[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[t2], 0, 0, 0);
+                    const v8 kf = *reinterpret_cast<const v8*>(sK + (t2 * 32 + lr) * LDK + ks * 16 + lg * 8);
+                    s[t2] = O::mma(kf, qf[ks], s[t2]);
                 }
             }
 
@@ -288,14 +322,14 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
             m_run = m_new;
 
             float lsum = 0.f;
-            half8 pf[4];
+            v8 pf[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float pv = __builtin_amdgcn_exp2f(s[t >> 1][8 * (t & 1) + e] - m_use);
                     lsum += pv;
-                    pf[t][e] = to_half(pv);
+                    pf[t][e] = static_cast<E>(pv);
                 }
             }
             l_run = l_run * corr + lsum;
@@ -312,13 +346,13 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
                 const int kb = 32 * (t >> 1) + 16 * (t & 1) + 4 * lg;
 #pragma unroll
                 for (int j = 0; j < HT; ++j) {
-                    const _Float16* vrow = sVt + (j * 32 + lr) * LDV + kb;
-                    const half4 lo = *reinterpret_cast<const half4*>(vrow);
-                    const half4 hi = *reinterpret_cast<const half4*>(vrow + 8);
-                    half8 vf;
+                    const E* vrow = sVt + (j * 32 + lr) * LDV + kb;
+                    const v4 lo = *reinterpret_cast<const v4*>(vrow);
+                    const v4 hi = *reinterpret_cast<const v4*>(vrow + 8);
+                    v8 vf;
                     vf[0] = lo[0]; vf[1] = lo[1]; vf[2] = lo[2]; vf[3] = lo[3];
                     vf[4] = hi[0]; vf[5] = hi[1]; vf[6] = hi[2]; vf[7] = hi[3];
-                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], o[j], 0, 0, 0);
+                    o[j] = O::mma(vf, pf[t], o[j]);
                 }
             }
         }
@@ -358,31 +392,30 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
     }
 }
 
-template <int HD, int NW, bool IN_F32, bool OUT_F32>
+template <int HD, int NW, bool IN_F32, bool OUT_F32, bool BF16>
 void launch_attn(const AttnParams& p, hipStream_t stream) {
     const int64_t blocks = static_cast<int64_t>(p.nqb) * p.B * p.H;
-    hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, IN_F32, OUT_F32>), dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, IN_F32, OUT_F32, BF16>), dim3(static_cast<unsigned>(blocks)),
                        dim3(NW * 64), 0, stream, p);
 }
 
 int waves_for(int S) { return attn_waves_for(S); }
-int query_blocks(int S) { return attn_query_blocks(S); }
 
-template <int HD, bool IN_F32, bool OUT_F32>
+template <int HD, bool IN_F32, bool OUT_F32, bool BF16>
 void launch_nw(const AttnParams& p, hipStream_t stream) {
     switch (waves_for(p.S)) {
-        case 1: launch_attn<HD, 1, IN_F32, OUT_F32>(p, stream); break;
-        case 2: launch_attn<HD, 2, IN_F32, OUT_F32>(p, stream); break;
-        default: launch_attn<HD, 4, IN_F32, OUT_F32>(p, stream); break;
+        case 1: launch_attn<HD, 1, IN_F32, OUT_F32, BF16>(p, stream); break;
+        case 2: launch_attn<HD, 2, IN_F32, OUT_F32, BF16>(p, stream); break;
+        default: launch_attn<HD, 4, IN_F32, OUT_F32, BF16>(p, stream); break;
     }
 }
 
-template <bool IN_F32, bool OUT_F32>
+template <bool IN_F32, bool OUT_F32, bool BF16>
 bool launch_hd(int hd, const AttnParams& p, hipStream_t stream) {
     switch (hd) {
-        case 32: launch_nw<32, IN_F32, OUT_F32>(p, stream); return true;
-        case 64: launch_nw<64, IN_F32, OUT_F32>(p, stream); return true;
-        case 128: launch_nw<128, IN_F32, OUT_F32>(p, stream); return true;
+        case 32: launch_nw<32, IN_F32, OUT_F32, BF16>(p, stream); return true;
+        case 64: launch_nw<64, IN_F32, OUT_F32, BF16>(p, stream); return true;
+        case 128: launch_nw<128, IN_F32, OUT_F32, BF16>(p, stream); return true;
         default: return false;
     }
 }
@@ -436,19 +469,26 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
     DOTL_REQUIRE(qkv_strides != nullptr, "fused_attention_forward: strides required");
 
     // The impl x precision vocabulary of the reference
-    // (reference csrc/attention_dispatch.cuh:221-304): a forced impl asking for
-    // arithmetic it does not have is an error; "tile" is an NVIDIA programming
-    // model with no counterpart here and always reports unavailable.
+    // (reference csrc/attention_dispatch.cuh:219-304, attention_wmma.cuh:2043-2084):
+    //   * scalar (impl 1) is the exact fp32 kernel and has only fp32;
+    //   * wmma (impl 2) has no fp32. fp16 tensors contract in fp16 whatever the
+    //     precision; fp32 tensors narrow to the requested type, "auto" meaning
+    //     the process-wide fp16 knob (on: fp16, off: tf32). gfx950 has no tf32
+    //     matrix instruction, so a forced wmma declines tf32;
+    //   * auto (impl 0): fp32 -> scalar; otherwise the MFMA kernel where it
+    //     covers the head_dim and arithmetic, else the scalar kernel (whose
+    //     fp32 arithmetic is at least as precise as the request);
+    //   * "tile" is an NVIDIA programming model with no counterpart here and
+    //     always reports unavailable.
     if (impl == 3) {
         set_error("fused_attention_forward: impl=3 (tile) is not available in this build: the "
                   "tile programming model has no gfx950 counterpart");
         return DOTL_E_UNSUPPORTED;
     }
-    int prec = precision;
-    if (prec == 0) prec = attention_fp16_default() ? 3 : 1;
-    if (impl == 2 && prec == 1) {
+    if (impl == 2 && precision == 1) {
         set_error("fused_attention_forward: --attn-impl wmma has no fp32 arithmetic. It supports: "
-                  "fp16. Note this is the MATH type, not the tensor dtype.");
+                  "tf32 (declined on gfx950), fp16, bf16. Note this is the MATH type, not the "
+                  "tensor dtype.");
         return DOTL_E_UNSUPPORTED;
     }
     if (impl == 1 && precision != 0 && precision != 1) {
@@ -456,12 +496,39 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
                   precision_name(precision) + " arithmetic. It supports: fp32.");
         return DOTL_E_UNSUPPORTED;
     }
-    if (prec != 3 || impl == 1) {
+    // The MFMA arithmetic this call would get: 3 fp16, 4 bf16, 2 tf32 (none).
+    int mfma_prec = 3;
+    if (dtype == DOTL_F32) {
+        mfma_prec = precision == 0 ? (attention_fp16_default() ? 3 : 2) : precision;
+    }
+    const bool mfma_hd = head_dim == 32 || head_dim == 64 || head_dim == 128;
+    const bool mfma_ok = mfma_hd && (mfma_prec == 3 || mfma_prec == 4);
+    bool use_scalar;
+    if (impl == 1 || (impl == 0 && precision == 1)) {
+        use_scalar = true;
+    } else if (impl == 2) {
+        if (!mfma_ok) {
+            char buf[320];
+            std::snprintf(buf, sizeof(buf),
+                          "fused_attention_forward: impl=2 (wmma), precision=%s does not cover "
+                          "head_dim=%d%s; the MFMA kernel covers head_dim in {32, 64, 128} with "
+                          "fp16 or bf16 operands",
+                          precision_name(mfma_prec), head_dim,
+                          mfma_prec == 2 ? " (gfx950 has no tf32 matrix instruction)" : "");
+            set_error(buf);
+            return DOTL_DECLINED;
+        }
+        use_scalar = false;
+    } else {
+        use_scalar = !mfma_ok;
+    }
+    if (use_scalar && head_dim > kMaxScalarHeadDim) {
         char buf[256];
         std::snprintf(buf, sizeof(buf),
-                      "fused_attention_forward: impl=%d (%s), precision=%s is not covered by this "
-                      "build: the MFMA kernel contracts in fp16",
-                      impl, impl_name(impl), precision_name(prec));
+                      "fused_attention_forward: impl=%d (%s), precision=%s does not cover "
+                      "head_dim=%d; the scalar kernel covers head_dim up to %d",
+                      impl, impl_name(impl), precision_name(precision), head_dim,
+                      kMaxScalarHeadDim);
         set_error(buf);
         return DOTL_DECLINED;
     }
@@ -478,8 +545,8 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
                             static_cast<uintptr_t>(qkv_strides[0] * es) |
                             static_cast<uintptr_t>(qkv_strides[1] * es) |
                             static_cast<uintptr_t>(qkv_strides[2] * es);
-    DOTL_REQUIRE(align % 16 == 0,
-                 "fused_attention_forward: q/k/v rows must be 16-byte aligned");
+    DOTL_REQUIRE(use_scalar || align % 16 == 0,
+                 "fused_attention_forward: q/k/v rows must be 16-byte aligned for the MFMA kernel");
 
     AttnParams p{};
     p.q = q; p.k = k; p.v = v;
@@ -501,33 +568,35 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
         if (fnw == 1 || fnw == 2 || fnw == 4) nw = fnw;
         if (fns >= 1 && fns <= 4) ns = fns;
     }
-    p.nqb = (S + 32 * nw - 1) / (32 * nw);
+    p.nqb = use_scalar ? attn_scalar_query_blocks(S, head_dim) : (S + 32 * nw - 1) / (32 * nw);
     DOTL_REQUIRE(static_cast<int64_t>(p.nqb) * B * H <= 0x7fffffff,
                  "fused_attention_forward: grid too large");
     p.scale_log2 = static_cast<float>(scale * 1.4426950408889634);
     const hipStream_t st = as_stream(stream);
 
-    bool launched;
     const bool in32 = dtype == DOTL_F32;
     const bool out32 = out_dtype == DOTL_F32;
-    if (in32) {
-        launched = out32 ? launch_hd<true, true>(head_dim, p, st) : launch_hd<true, false>(head_dim, p, st);
+    bool launched;
+    if (use_scalar) {
+        launched = launch_attn_scalar(p, head_dim, in32, out32, static_cast<float>(scale), st);
+    } else if (in32 && mfma_prec == 4) {
+        launched = out32 ? launch_hd<true, true, true>(head_dim, p, st)
+                         : launch_hd<true, false, true>(head_dim, p, st);
+    } else if (in32) {
+        launched = out32 ? launch_hd<true, true, false>(head_dim, p, st)
+                         : launch_hd<true, false, false>(head_dim, p, st);
     } else if (attention_cp_async_mode() != 0) {
         // fp16 q/k/v: K/V tiles streamed into LDS asynchronously (the
         // reference's cp_async staging; mode 0 selects the register-staged
         // kernel below).
         launched = launch_attn_dma(p, head_dim, out32, nw, ns, st);
     } else {
-        launched = out32 ? launch_hd<false, true>(head_dim, p, st) : launch_hd<false, false>(head_dim, p, st);
+        launched = out32 ? launch_hd<false, true, false>(head_dim, p, st)
+                         : launch_hd<false, false, false>(head_dim, p, st);
     }
     if (!launched) {
-        char buf[256];
-        std::snprintf(buf, sizeof(buf),
-                      "fused_attention_forward: impl=%d (%s), precision=%s does not cover "
-                      "head_dim=%d; the MFMA kernel covers head_dim in {32, 64, 128}",
-                      impl, impl_name(impl), precision_name(prec), head_dim);
-        set_error(buf);
-        return DOTL_DECLINED;
+        set_error("fused_attention_forward: no kernel instance for this shape");
+        return DOTL_E_INVALID;
     }
     return check_launch("fused_attention_forward");
 }

@@ -37,4 +37,13 @@ inline int attn_query_blocks(int S) {
 bool launch_attn_dma(const AttnParams& p, int head_dim, bool out_f32, int nw, int ns,
                      hipStream_t stream);
 
+// The exact fp32 kernel (attention_scalar.hip): q/k/v fp16 or fp32, any
+// head_dim in [1, kMaxScalarHeadDim], `scale` applied to the raw dot
+// products. Sizes its own grid (p.nqb is ignored); false when head_dim is
+// out of range.
+constexpr int kMaxScalarHeadDim = 2048;
+bool launch_attn_scalar(const AttnParams& p, int head_dim, bool in_f32, bool out_f32,
+                        float scale, hipStream_t stream);
+int attn_scalar_query_blocks(int S, int head_dim);
+
 }  // namespace dotl

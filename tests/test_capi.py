@@ -82,8 +82,21 @@ def test_attention_vocabulary_checks(lib):
     assert b"tile" in lib.dotl_last_error()
     # a forced wmma with fp32 arithmetic is a category error
     assert _attn(lib, impl=2, prec=1) == -3
-    # scalar (exact fp32) is not built here: declined, the caller raises
-    assert _attn(lib, impl=1) == 1
+    # scalar (the exact fp32 kernel) has only fp32 arithmetic
+    assert _attn(lib, impl=1, prec=3) == -3
+    assert b"scalar has no fp16" in lib.dotl_last_error()
+    # ... and covers head_dim up to 2048; an empty problem launches nothing
+    assert _attn(lib, impl=1, hd=2049) == 1
+    assert _attn(lib, impl=1, hd=2048) == 0
+    assert _attn(lib, impl=1, hd=3) == 0
+    # a forced MFMA kernel declines head dims it has no tile for, and tf32
+    # (no tf32 matrix instruction on gfx950) for fp32 tensors
+    assert _attn(lib, impl=2, hd=48) == 1
+    assert _attn(lib, impl=2, dtype=0, prec=2) == 1
+    assert b"tf32" in lib.dotl_last_error()
+    # auto takes the exact kernel for those instead
+    assert _attn(lib, impl=0, hd=48) == 0
+    assert _attn(lib, impl=0, dtype=0, prec=2) == 0
     # an empty problem on the covered path launches nothing
     assert _attn(lib, S=0) == 0
     # packed sequences write the packed layout: out_layout 0 is refused

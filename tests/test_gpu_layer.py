@@ -103,6 +103,33 @@ def test_layer_precision_knobs(kernels):
 
 
 @pytest.mark.parametrize("name", ["C1", "C2"])
+def test_layer_fp32_class_end_to_end(kernels, name):
+    """Exact fp32 attention (ATTENTION_PRECISION="fp32", the scalar kernel; at C2
+    over packed rows) with the split fp16x3 GEMMs: the whole layer at fp32-class
+    error. Bound: 5e-5 absolute, against ~1e-3 for the fp16 path."""
+    cfg = CONFIGS[name]
+    x, mask, params = make_case(cfg, batch=2)
+    ref = reference_layer(x, mask, params, cfg).numpy()
+    saved = (ocfg.ATTENTION_PRECISION, ocfg.LINEAR_BIAS, ocfg.LINEAR_GELU)
+    try:
+        ocfg.LINEAR_BIAS, ocfg.LINEAR_GELU = "tf32", "tf32"
+        half_attn, _ = _run_gpu(cfg, x, mask, params)
+        ocfg.ATTENTION_PRECISION = "fp32"
+        okernels.fallback_counts.clear()
+        exact, _ = _run_gpu(cfg, x, mask, params)
+        assert not okernels.fallback_counts, dict(okernels.fallback_counts)
+    finally:
+        ocfg.ATTENTION_PRECISION, ocfg.LINEAR_BIAS, ocfg.LINEAR_GELU = saved
+    r_half, r_exact = compare_outputs(ref, half_attn), compare_outputs(ref, exact)
+    print(f"[fp32-class] {name}: fp16 attention max_abs={r_half.max_abs_error:.3e}, "
+          f"fp32 attention max_abs={r_exact.max_abs_error:.3e}", flush=True)
+    assert r_exact.passed and r_exact.max_abs_error < 5e-5
+    assert r_exact.max_abs_error < r_half.max_abs_error
+    if mask is not None:
+        assert np.all(exact[~mask] == 0.0)
+
+
+@pytest.mark.parametrize("name", ["C1", "C2"])
 def test_graph_replay_matches_eager(kernels, name):
     """Captured forward == eager forward exactly, on repeated replays with eager
     work and synchronisations between them, and fresh inputs reach the graph."""

@@ -327,8 +327,10 @@ def test_attention_refusals(kernels):
     with pytest.raises(RuntimeError, match="fp32"):
         kernels.fused_attention_forward(q, q, q, None, False, 0.125, 2, 1, 1)
     with pytest.raises(RuntimeError, match="head_dim"):
+        # a forced MFMA kernel declines a head_dim it has no tile for (auto
+        # would run the exact fp32 kernel instead)
         q48 = torch.randn(1, 1, 16, 48, device=DEV).half()
-        kernels.fused_attention_forward(q48, q48, q48, None, False, 0.125, 0, 1, 0)
+        kernels.fused_attention_forward(q48, q48, q48, None, False, 0.125, 2, 1, 0)
     with pytest.raises(RuntimeError):
         qb = q.bfloat16()
         kernels.fused_attention_forward(qb, qb, qb, None, False, 0.125, 0, 1, 0)
