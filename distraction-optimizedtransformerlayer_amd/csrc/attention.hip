@@ -600,12 +600,3 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
     }
     return check_launch("fused_attention_forward");
 }
-
-extern "C" int dotl_ffn_block(const float*, const float*, const float*, const float*,
-                              const float*, const float*, const float*, const float*,
-                              const float*, const float*, float*, float*, int64_t, int64_t,
-                              int64_t, double, void*) {
-    dotl::clear_error();
-    dotl::set_error("fused_ffn_block: no fused block in this build; run the unfused chain");
-    return DOTL_DECLINED;
-}

@@ -82,6 +82,25 @@ __device__ __forceinline__ float gelu_erf(float x) {
     return x >= 0.f ? x - h : h;
 }
 
+// LayerNorm arithmetic shared by every kernel that normalises a row, each
+// multiply-add written as an explicit fmaf. Left to the compiler, a sum of
+// two products contracts either way round (fma(a, a, b*b) or fma(b, b, a*a)),
+// and two kernels computing the same expression could differ in the last bit.
+__device__ __forceinline__ float ln_sq4(float d0, float d1, float d2, float d3) {
+    return fmaf(d1, d1, d0 * d0) + fmaf(d3, d3, d2 * d2);
+}
+// Biased variance from the centred sums: E[d^2] - E[d]^2, clamped at 0.
+__device__ __forceinline__ float ln_var(float sd2, float delta, float inv_d) {
+    return fmaxf(fmaf(-delta, delta, sd2 * inv_d), 0.f);
+}
+// (x - mean) * rstd * w + b, with x - mean formed as (x - mean_est) - delta:
+// x - mean_est is exact for x near the mean, whereas forming mean_est + delta
+// first would round the mean to ulp(mean).
+__device__ __forceinline__ float ln_out(float v, float mean_est, float delta, float rstd,
+                                        float w, float b) {
+    return fmaf(((v - mean_est) - delta) * rstd, w, b);
+}
+
 // fp32 -> fp16 with round-to-nearest-even (the hardware conversion).
 __device__ __forceinline__ _Float16 to_half(float x) { return static_cast<_Float16>(x); }
 

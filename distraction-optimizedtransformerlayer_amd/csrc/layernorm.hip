@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
                 const float d0 = v[c].x - mean_est, d1 = v[c].y - mean_est;
                 const float d2 = v[c].z - mean_est, d3 = v[c].w - mean_est;
                 sd += (d0 + d1) + (d2 + d3);
-                sd2 += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+                sd2 += ln_sq4(d0, d1, d2, d3);
             }
         }
 #pragma unroll
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
             sd2 += __shfl_xor(sd2, off, kWave);
         }
         const float delta = sd * inv_d;
-        const float var = fmaxf(sd2 * inv_d - delta * delta, 0.f);
+        const float var = ln_var(sd2, delta, inv_d);
         const float rstd = 1.0f / sqrtf(var + eps);
 
         // x - mean as (x - m) - delta: x - m is exact (both near the mean),
@@ -141,10 +141,10 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
                 const float4 ww = *reinterpret_cast<const float4*>(w + col);
                 const float4 bb = *reinterpret_cast<const float4*>(b + col);
                 float4 o;
-                o.x = ((v[c].x - mean_est) - delta) * rstd * ww.x + bb.x;
-                o.y = ((v[c].y - mean_est) - delta) * rstd * ww.y + bb.y;
-                o.z = ((v[c].z - mean_est) - delta) * rstd * ww.z + bb.z;
-                o.w = ((v[c].w - mean_est) - delta) * rstd * ww.w + bb.w;
+                o.x = ln_out(v[c].x, mean_est, delta, rstd, ww.x, bb.x);
+                o.y = ln_out(v[c].y, mean_est, delta, rstd, ww.y, bb.y);
+                o.z = ln_out(v[c].z, mean_est, delta, rstd, ww.z, bb.z);
+                o.w = ln_out(v[c].w, mean_est, delta, rstd, ww.w, bb.w);
                 if constexpr (NORMED == DOTL_F16 || NORMED == DOTL_F16X2) {
                     half4 h;
                     h[0] = to_half(o.x); h[1] = to_half(o.y);
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256) void layernorm_scalar_kernel(
             if (e * 64 + lane < D) {
                 const float d = v[e] - mean_est;
                 sd += d;
-                sd2 += d * d;
+                sd2 = fmaf(d, d, sd2);
             }
         }
 #pragma unroll
@@ -228,14 +228,14 @@ __global__ __launch_bounds__(256) void layernorm_scalar_kernel(
             sd2 += __shfl_xor(sd2, off, kWave);
         }
         const float delta = sd * inv_d;
-        const float var = fmaxf(sd2 * inv_d - delta * delta, 0.f);
+        const float var = ln_var(sd2, delta, inv_d);
         const float rstd = 1.0f / sqrtf(var + eps);
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
             const int col = e * 64 + lane;
             if (col < D) {
                 if constexpr (WRITE_XNEW) x_new[base + col] = v[e];
-                const float o = ((v[e] - mean_est) - delta) * rstd * w[col] + b[col];
+                const float o = ln_out(v[e], mean_est, delta, rstd, w[col], b[col]);
                 if constexpr (NORMED == DOTL_F16 || NORMED == DOTL_F16X2) {
                     const _Float16 h = to_half(o);
                     static_cast<_Float16*>(normed)[base + col] = h;

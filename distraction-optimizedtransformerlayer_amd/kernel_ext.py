@@ -551,20 +551,42 @@ class Kernels:
 
     def fused_ffn_block(self, x, attn_out, norm1_w, norm1_b, ffn_in_w, ffn_in_b, ffn_out_w,
                         ffn_out_b, norm2_w, norm2_b, eps):
-        self._require_cuda("fused_ffn_block", x, attn_out)
+        """[x2, normed2] of the fused post-attention block, or [] when the widths
+        are not covered (reference csrc/ffn_block.cuh:270-311). fp32 tensors;
+        the weights are narrowed to fp16 through the same cache the GEMMs use."""
+        import torch
+
+        who = "fused_ffn_block"
+        self._require_cuda(who, x, attn_out)
         if tuple(x.shape) != tuple(attn_out.shape):
-            raise RuntimeError(f"fused_ffn_block: x and attn_out must match, got "
+            raise RuntimeError(f"{who}: x and attn_out must match, got "
                                f"{tuple(x.shape)} and {tuple(attn_out.shape)}")
-        D = x.shape[-1]
-        F = ffn_in_w.shape[0]
-        args = [t.data_ptr() for t in (x, attn_out, norm1_w, norm1_b, ffn_in_w, ffn_in_b,
-                                        ffn_out_w, ffn_out_b, norm2_w, norm2_b)]
+        if x.dtype != torch.float32 or attn_out.dtype != torch.float32:
+            raise RuntimeError(f"{who}: float32 only, got {x.dtype}")
+        if ffn_in_w.dim() != 2 or ffn_out_w.dim() != 2:
+            raise RuntimeError(f"{who}: ffn weights must be 2-D")
+        D = int(x.shape[-1])
+        F = int(ffn_in_w.shape[0])
+        if (tuple(ffn_in_w.shape) != (F, D) or tuple(ffn_out_w.shape) != (D, F)):
+            raise RuntimeError(f"{who}: weight shapes disagree with d_model={D} ffn_dim={F}")
+        if D > 128 or F > 128 or D % 8 or F % 8:
+            return []
+        xc, ac = x.contiguous(), attn_out.contiguous()
+        rows = xc.numel() // D
+        win, _ = self.weight_half(ffn_in_w, False)
+        wout, _ = self.weight_half(ffn_out_w, False)
+        params = [t.contiguous().float() for t in (norm1_w, norm1_b, ffn_in_b, ffn_out_b,
+                                                    norm2_w, norm2_b)]
+        x_out = torch.empty_like(xc)
+        normed = torch.empty_like(xc)
         rc = self._check(self._lib.dotl_ffn_block(
-            *args, None, None, x.numel() // D, D, F, float(eps), self._stream(x.device)))
+            xc.data_ptr(), ac.data_ptr(), params[0].data_ptr(), params[1].data_ptr(),
+            win.data_ptr(), params[2].data_ptr(), wout.data_ptr(), params[3].data_ptr(),
+            params[4].data_ptr(), params[5].data_ptr(), x_out.data_ptr(), normed.data_ptr(),
+            rows, D, F, float(eps), self._stream(x.device)))
         if rc == DOTL_DECLINED:
             return []
-        raise RuntimeError("fused_ffn_block: the library launched a block this loader "
-                           "allocated no outputs for")
+        return [x_out, normed]
 
     # -- knobs (reference csrc/fused_attention.cu:157-366) -------------------------
 

@@ -86,8 +86,11 @@ _NORMED_FP16_MAX_K = 1 << 30
 # layer's widest intermediate.
 GELU_FP16 = "auto"
 
-# Fused post-attention block. This build's fused_ffn_block declines every
-# shape, so "auto" and "force" both end in the unfused chain.
+# Fused post-attention block (add+LN, Linear+GELU, Linear, add+LN in one
+# kernel, kernel_ext.fused_ffn_block) on the unpadded path: "auto" up to
+# d_model _FFN_BLOCK_MAX_D (the reference's gate), "force" at any width the
+# kernel covers (d_model and d_ff up to 128), "off" never. The kernel's
+# outputs equal the unfused chain's, so this is a speed choice only.
 FFN_BLOCK = "auto"
 _FFN_BLOCK_MAX_D = 64
 

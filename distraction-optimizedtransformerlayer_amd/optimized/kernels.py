@@ -260,8 +260,20 @@ def _linear_bias(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Ten
 
 
 def _ffn_block(x, attn_out, norm1, ffn_in, ffn_out, norm2):
-    """The fused post-attention block, or None to run it unfused."""
+    """The fused post-attention block, or None to run it unfused
+    (reference optimized/kernels.py:269-294).
+
+    The kernel's arithmetic is the default unfused chain's (fp16 LayerNorm
+    output, fp16 GEMM operands, fp16 GELU output), so it is used only while
+    the knobs select exactly that chain: a request for the split fp16x3
+    GEMMs, or for fp32 edges, runs unfused.
+    """
     if config.FFN_BLOCK == "off":
+        return None
+    if (config.LINEAR_GELU != "auto" or config.LINEAR_BIAS != "auto"
+            or config.NORMED_FP16 == "off" or config.GELU_FP16 == "off"):
+        return None
+    if ffn_in.bias is None or ffn_out.bias is None or x.dtype != torch.float32:
         return None
     if config.FFN_BLOCK != "force" and x.shape[-1] > config._FFN_BLOCK_MAX_D:
         return None

@@ -185,15 +185,24 @@ int dotl_attention_forward(const void* q, const void* k, const void* v, int dtyp
                            const int32_t* cu_seqlens, void* stream);
 
 /*
- * Fused post-attention block (add+LN, Linear+GELU, Linear, add+LN).
- * Replaces fused_ffn_block (reference csrc/ffn_block.cuh:270-311), whose
- * contract is "run it or decline": this build declines every shape
- * (DOTL_DECLINED), and the caller runs the unfused chain -- which the
- * reference's own gate also does at every configured width above 64.
+ * Fused post-attention block. Replaces fused_ffn_block (reference
+ * csrc/ffn_block.cuh:270-311):
+ *   x1 = x + attn_out;            n1 = LayerNorm(x1; norm1_w, norm1_b)
+ *   h  = GELU(n1 W_in^T + b_in);  x_out = x1 + h W_out^T + b_out
+ *   normed_out = LayerNorm(x_out; norm2_w, norm2_b)
+ * x, attn_out, x_out, normed_out fp32 [rows, D]; W_in [F, D] and W_out
+ * [D, F] given as fp16 (the fp16-operand GEMMs' narrowing of the fp32
+ * weights, RNE); biases and LayerNorm parameters fp32. The arithmetic is the
+ * unfused chain's (fp16 operands, fp32 accumulation, h rounded to fp16), so
+ * the outputs equal that chain's bit for bit.
+ * Covers D and F up to 128 in multiples of 8 (the reference instantiates
+ * D == F in {16, 32, 48, 64, 128}); other widths return DOTL_DECLINED and the
+ * caller runs the unfused chain, as the reference's empty-list decline.
+ * Tensors 16-byte aligned.
  */
 int dotl_ffn_block(const float* x, const float* attn_out, const float* norm1_w,
-                   const float* norm1_b, const float* ffn_in_w, const float* ffn_in_b,
-                   const float* ffn_out_w, const float* ffn_out_b, const float* norm2_w,
+                   const float* norm1_b, const void* ffn_in_w_half, const float* ffn_in_b,
+                   const void* ffn_out_w_half, const float* ffn_out_b, const float* norm2_w,
                    const float* norm2_b, float* x_out, float* normed_out, int64_t rows,
                    int64_t D, int64_t F, double eps, void* stream);
 

@@ -116,9 +116,19 @@ def test_layernorm_checks(lib):
     assert ln(1, 64, row_index=ctypes.cast(idx, ctypes.c_void_p), in_rows=-1) == -1
 
 
-def test_ffn_block_declines(lib):
-    rc = lib.dotl_ffn_block(*([None] * 12), 16, 64, 64, ctypes.c_double(1e-5), None)
-    assert rc == 1
+def test_ffn_block_checks(lib):
+    def ffn(rows, D, F):
+        return lib.dotl_ffn_block(*([None] * 12), rows, D, F, ctypes.c_double(1e-5), None)
+
+    # widths past 128, or not multiples of 8: declined, the caller runs the chain
+    assert ffn(16, 256, 256) == 1
+    assert ffn(16, 128, 512) == 1
+    assert ffn(16, 60, 64) == 1
+    assert b"not covered" in lib.dotl_last_error()
+    # covered widths: an empty problem launches nothing; null tensors are an error
+    assert ffn(0, 64, 64) == 0
+    assert ffn(16, 48, 48) == -1
+    assert ffn(-1, 64, 64) == -1
 
 
 def test_knobs_roundtrip(lib):
