@@ -164,7 +164,8 @@ def layer_ops(cfg, model, x, mask):
             planes = ln1()
             ln1_bytes = T * D * 8.0
         qkv_w, qkv_b = attn._get_qkv_weight()
-        qkv = kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True)
+        split_w = ocfg.QKV_PRECISION == "fp16x3"
+        qkv = kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True, split_weight=split_w)
         if packing is not None:
             q, k, v = qkv.view(R, 3, H, hd).unbind(1)
             attn_fn = lambda: kx.fused_attention_forward(q, k, v, None, cfg.causal, scale, 0, 1, 0,  # noqa: E731
@@ -195,13 +196,13 @@ def layer_ops(cfg, model, x, mask):
     # Compulsory HBM bytes per call: every operand read once, every output
     # written once (the fp16 weight copies the GEMMs read; the split QKV
     # weight is two fp16 planes).
-    wq16 = 2.0 * 2 * qkv_w.numel()
+    wq16 = 2.0 * (2 if split_w else 1) * qkv_w.numel()   # fp16 hi (+ lo) planes of W
     w16 = lambda lin: 2.0 * lin.weight.numel() + nb(lin.bias)  # noqa: E731
     cu_bytes = nb(packing.cu) if packing is not None else nb(mask)
     ops = {
         "layernorm (norm1, split-fp16 out)": (ln1, "hbm", ln1_bytes, ln1_bytes),
-        "linear qkv (fp16x3, fp16 out)": (
-            lambda: kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True),
+        f"linear qkv ({ocfg.QKV_PRECISION}, fp16 out)": (
+            lambda: kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True, split_weight=split_w),
             "mfma", 2.0 * R * D * 3 * D, nb(planes, qkv_b, qkv) + wq16),
         "attention": (attn_fn, "mfma", attention_useful_flops(cfg, L), nb(qkv, ctx) + cu_bytes),
         "linear out_proj": (
@@ -440,6 +441,7 @@ def _main(out):
         return 2
     if kernel_ext.get_kernels() is None:
         raise RuntimeError(f"libdotl_hip.so did not load: {kernel_ext.load_error()}")
+    from optimized import config as ocfg
 
     log(f"[bench] device={torch.cuda.get_device_name(0)} config={args.config} "
         f"steps={args.steps} warmup={args.warmup} graph={args.graph}")
@@ -506,7 +508,10 @@ def _main(out):
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32 I/O; fp16 MFMA operands, fp32 accumulate (QKV: split fp16x3)",
+        "dtype": ("fp32 I/O; fp16 MFMA operands, fp32 accumulate (QKV: "
+                  + {"fp16x2": "LayerNorm output as split fp16 hi+lo, two passes",
+                     "fp16x3": "split fp16x3, three passes",
+                     "fp16": "one fp16 pass"}[ocfg.QKV_PRECISION] + ")"),
         "data": "synthetic (seeded Xavier weights, N(0,1) x, key-padding lengths)",
         "config": {"workload": f"{cfg.name}: single-layer forward B={cfg.batch_size} "
                                f"S={cfg.seq_len} d_model={cfg.d_model} heads={cfg.num_heads} "

@@ -39,7 +39,7 @@ namespace dotl {
 int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes);
 bool launch_gemm_dma(const _Float16* A, const _Float16* Alo, const _Float16* W,
                      const _Float16* Wlo, const float* bias, void* C, int64_t M, int64_t N,
-                     int64_t K, int passes, int act, bool out_f16, int tile, hipStream_t stream);
+                     int64_t K, int mode, int act, bool out_f16, int tile, hipStream_t stream);
 
 namespace {
 
@@ -439,7 +439,10 @@ extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const v
                  "%s: x must be float32, float16 or split float16", who);
     DOTL_REQUIRE(out_dtype == DOTL_F32 || out_dtype == DOTL_F16, "%s: out must be float32 or float16", who);
     DOTL_REQUIRE(act == DOTL_ACT_NONE || act == DOTL_ACT_GELU, "%s: unknown activation %d", who, act);
-    DOTL_REQUIRE(math == DOTL_MATH_FP16 || math == DOTL_MATH_FP16X3, "%s: unknown math %d", who, math);
+    DOTL_REQUIRE(math == DOTL_MATH_FP16 || math == DOTL_MATH_FP16X3 || math == DOTL_MATH_FP16X2,
+                 "%s: unknown math %d", who, math);
+    DOTL_REQUIRE(math != DOTL_MATH_FP16X2 || x_dtype == DOTL_F16X2,
+                 "%s: the fp16x2 math takes x as split fp16 planes", who);
     DOTL_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative extent", who);
     if (K % 8 != 0 || K == 0) {
         set_error(std::string(who) + ": K must be a positive multiple of 8 for 16-byte staging");
@@ -452,7 +455,7 @@ extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const v
     DOTL_REQUIRE(math != DOTL_MATH_FP16X3 || w_lo != nullptr,
                  "%s: the fp16x3 math needs the split weight residual", who);
     DOTL_REQUIRE(((M + 63) / 64) * ((N + 63) / 64) <= 0x7fffffff, "%s: too large", who);
-    DOTL_REQUIRE(tile == -1 || (tile >= 0 && tile <= 8) || (tile >= 100 && tile <= 104),
+    DOTL_REQUIRE(tile == -1 || (tile >= 0 && tile <= 13) || (tile >= 100 && tile <= 104),
                  "%s: unknown tile id %d", who, tile);
     if (M == 0 || N == 0) return DOTL_OK;
     DOTL_REQUIRE(x && w_hi && bias && out, "%s: null pointer", who);
@@ -462,21 +465,28 @@ extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const v
     const bool of16 = out_dtype == DOTL_F16;
     const bool split = math == DOTL_MATH_FP16X3;
 
-    // LDS-DMA pipelined kernel: fp16 operands, K a multiple of 64.
+    // LDS-DMA pipelined kernel: fp16 operands, K a multiple of 64, each
+    // operand under 4 GiB (its per-lane DMA offsets are 32-bit).
     const bool force_staged = tile >= 100;
-    if (!force_staged && x_dtype != DOTL_F32 && K % 64 == 0) {
+    const bool dma_fits = M * K * 2 < (int64_t{1} << 32) && N * K * 2 < (int64_t{1} << 32);
+    if (!force_staged && x_dtype != DOTL_F32 && K % 64 == 0 && dma_fits) {
         const _Float16* xh = static_cast<const _Float16*>(x);
         const _Float16* xl = x_dtype == DOTL_F16X2 ? xh + M * K : nullptr;
-        const int passes = !split ? 1 : (x_dtype == DOTL_F16X2 ? 3 : 2);
+        // split modes: bit 0 lo(W), bit 1 lo(x)
+        const int mode = math == DOTL_MATH_FP16X2 ? 2
+                         : (!split ? 0 : (x_dtype == DOTL_F16X2 ? 3 : 1));
+        const int passes = 1 + (mode & 1) + ((mode >> 1) & 1);
         const int t = tile < 0 ? pick_dma_tile(M, N, K, passes) : tile;
         if (launch_gemm_dma(xh, xl, static_cast<const _Float16*>(w_hi),
-                            static_cast<const _Float16*>(w_lo), bias, out, M, N, K, passes, act,
+                            static_cast<const _Float16*>(w_lo), bias, out, M, N, K, mode, act,
                             of16, t, as_stream(stream))) {
             return check_launch(who);
         }
-        DOTL_REQUIRE(x_dtype != DOTL_F16X2, "%s: tile id %d is not built for three passes", who, tile);
+        DOTL_REQUIRE(x_dtype != DOTL_F16X2, "%s: tile id %d is not built for split passes", who, tile);
     }
-    DOTL_REQUIRE(x_dtype != DOTL_F16X2, "%s: split-fp16 x is served by the pipelined kernel only", who);
+    DOTL_REQUIRE(x_dtype != DOTL_F16X2,
+                 "%s: split-fp16 x is served by the pipelined kernel only (K %% 64 == 0, operands "
+                 "under 4 GiB)", who);
 
     GemmArgs g{x, static_cast<const _Float16*>(w_hi), static_cast<const _Float16*>(w_lo), bias,
                out, M, N, K, as_stream(stream)};

@@ -24,15 +24,17 @@
 //     the 16 rows a fragment read touches then sit on 16 distinct 16-byte
 //     bank groups (chunk ^ (row / rows-per-256B) % chunks-per-row),
 //     conflict-free without padding (which would break the DMA's contiguous
-//     lane layout). The swizzle is applied on the global side: each DMA lane
-//     writes a fixed physical chunk and loads the logical chunk that maps
-//     there;
+//     lane layout; measured with SQ_LDS_BANK_CONFLICT on an LDS-only loop:
+//     zero, against 2-way for a 128-byte sweep and 4-way unswizzled). The
+//     swizzle is applied on the global side: each DMA lane writes a fixed
+//     physical chunk and loads the logical chunk that maps there;
 //   * rows past M (or N) are clamped to the last valid row -- those outputs
 //     are never stored -- so every DMA is in bounds and branch-free; K must
 //     be a multiple of 64 (no K tail);
-//   * PASSES = 1: x*W. 2: x*W + 2^-12 x*lo(W) (x exact in fp16). 3: also
-//     + 2^-12 lo(x)*W, with x given as fp16 hi/lo planes: fp32-class
-//     products on the fp16 matrix cores, in two fp32 accumulators;
+//   * MODE (bit 0: split W, bit 1: split x) sets the passes: 0 x*W; 1
+//     x*W + 2^-12 x*lo(W) (x exact in fp16); 2 hi(x)*W + 2^-12 lo(x)*W (x
+//     given as fp16 hi/lo planes, W in fp16); 3 all three products: the
+//     lo terms in a second fp32 accumulator;
 //   * 2 x 2 wavefronts, each a (BM/2) x (BN/2) block of 32x32 accumulators,
 //     issued as W x A^T so every accumulator holds a C^T tile: each lane then
 //     owns runs of 4 consecutive output columns of one row, and the epilogue
@@ -64,9 +66,11 @@ __device__ __forceinline__ void tile_of(int64_t id, int64_t nm, int64_t nn, int6
     nt = r / gsize;
 }
 
-template <int BM, int BN, int BK, int PASSES>
+template <int BM, int BN, int BK, int MODE>
 struct DmaLayout {
-    // rows of BK halves in one stage: A, W, then lo(W) (PASSES >= 2), lo(A) (PASSES == 3)
+    // rows of BK halves in one stage: A, W, then lo(W) (MODE & 1), lo(A) (MODE & 2)
+    static constexpr bool SW = (MODE & 1) != 0;
+    static constexpr bool SA = (MODE & 2) != 0;
     static constexpr int CPR = BK / 8;               // 16-byte chunks per row
     static constexpr int ROWS_PER_DMA = 64 / CPR;    // rows one wave instruction fills
     static constexpr int ROWS_PER_ROUND = 4 * ROWS_PER_DMA;
@@ -74,38 +78,27 @@ struct DmaLayout {
     static constexpr int A_ROW = 0;
     static constexpr int W_ROW = BM;
     static constexpr int WLO_ROW = BM + BN;
-    static constexpr int ALO_ROW = WLO_ROW + (PASSES >= 2 ? BN : 0);
-    static constexpr int ROWS = ALO_ROW + (PASSES == 3 ? BM : 0);
+    static constexpr int ALO_ROW = WLO_ROW + (SW ? BN : 0);
+    static constexpr int ROWS = ALO_ROW + (SA ? BM : 0);
     static constexpr int HALVES = ROWS * BK;
     static constexpr int LOADS = ROWS / ROWS_PER_ROUND;   // DMA instructions per wave per stage
     static_assert(BM % ROWS_PER_ROUND == 0 && BN % ROWS_PER_ROUND == 0, "rows per round");
     __device__ __forceinline__ static int swz(int row) { return (row / SWZ_DIV) % CPR; }
 };
 
-// Fill `ROWS` rows of a stage region from src (row pitch K halves), rows
-// past `nrows` clamped. One DMA instruction per wave per ROWS_PER_DMA rows.
-template <typename L, int ROWS>
-__device__ __forceinline__ void dma_rows(_Float16* lds_region, const _Float16* __restrict__ src,
-                                         int64_t row0, int64_t nrows, int64_t K, int64_t k0,
-                                         int wave, int lane) {
-    constexpr int BK = L::CPR * 8;
-    const int sub = lane / L::CPR;      // row within this wave's instruction
-    const int pc = lane % L::CPR;       // physical chunk this lane fills
-#pragma unroll
-    for (int i = 0; i < ROWS / L::ROWS_PER_ROUND; ++i) {
-        const int rbase = i * L::ROWS_PER_ROUND + wave * L::ROWS_PER_DMA;
-        const int r = rbase + sub;
-        const int lc = pc ^ L::swz(r);  // logical chunk it holds
-        int64_t gr = row0 + r;
-        gr = gr < nrows ? gr : nrows - 1;
-        const _Float16* g = src + gr * K + k0 + lc * 8;
-        dma16(g, lds_region + rbase * BK);  // wave-uniform destination
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, typename Fn>
+__device__ __forceinline__ void static_for(Fn&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
     }
 }
 
-template <int BM, int BN, int BK, int NS, int PASSES, int ACT, bool OUT_F16>
+template <int BM, int BN, int BK, int NS, int MODE, int ACT, bool OUT_F16>
 struct DmaGemm {
-    using L = DmaLayout<BM, BN, BK, PASSES>;
+    using L = DmaLayout<BM, BN, BK, MODE>;
+    static constexpr bool SPLIT = MODE != 0;
     static constexpr int WM = BM / 2, WN = BN / 2;
     static constexpr int TM = WM / 32, TN = WN / 32;
 
@@ -116,14 +109,56 @@ struct DmaGemm {
     int64_t M, N, K, m0, n0, nk;
     int wave, lane, wm, wn, lr, lg;
     floatx16 acc[TM][TN];
-    floatx16 acc2[PASSES > 1 ? TM : 1][PASSES > 1 ? TN : 1];
+    floatx16 acc2[SPLIT ? TM : 1][SPLIT ? TN : 1];
 
-    __device__ __forceinline__ void issue(_Float16* stage, int64_t kt) {
-        const int64_t k0 = kt * BK;
-        dma_rows<L, BM>(stage + L::A_ROW * BK, A, m0, M, K, k0, wave, lane);
-        dma_rows<L, BN>(stage + L::W_ROW * BK, W, n0, N, K, k0, wave, lane);
-        if constexpr (PASSES >= 2) dma_rows<L, BN>(stage + L::WLO_ROW * BK, Wlo, n0, N, K, k0, wave, lane);
-        if constexpr (PASSES == 3) dma_rows<L, BM>(stage + L::ALO_ROW * BK, Alo, m0, M, K, k0, wave, lane);
+    // A stage's DMA instructions (this wave's), in order: the rounds of A,
+    // W, lo(W) (MODE & 1), lo(A) (MODE & 2). Each lane's byte offset
+    // into its operand at k = 0 is computed once (row clamped to the last
+    // valid one, logical chunk from the swizzle); a stage then only adds the
+    // wave-uniform k offset to the operand's base, in scalar registers.
+    static constexpr int RA = BM / L::ROWS_PER_ROUND, RW = BN / L::ROWS_PER_ROUND;
+    static constexpr int NDMA = L::LOADS;
+    static constexpr int KS = BK / 16;
+    static constexpr int NWLO = L::SW ? RW : 0;
+    static constexpr int op_of(int d) {
+        return d < RA ? 0 : (d < RA + RW ? 1 : (d < RA + RW + NWLO ? 2 : 3));
+    }
+    static constexpr int round_of(int d) {
+        return d < RA ? d : (d < RA + RW ? d - RA : (d < RA + RW + NWLO ? d - RA - RW : d - RA - RW - NWLO));
+    }
+    static constexpr int region_row(int op) {
+        return op == 0 ? L::A_ROW : (op == 1 ? L::W_ROW : (op == 2 ? L::WLO_ROW : L::ALO_ROW));
+    }
+    unsigned doff[NDMA];
+
+    __device__ __forceinline__ void init_offsets() {
+        const int sub = lane / L::CPR;      // row within this wave's instruction
+        const int pc = lane % L::CPR;       // physical chunk this lane fills
+        static_for<0, NDMA>([&](auto dd) {
+            constexpr int D = decltype(dd)::value;
+            constexpr int op = op_of(D);
+            constexpr bool is_a = op == 0 || op == 3;
+            const int r = round_of(D) * L::ROWS_PER_ROUND + wave * L::ROWS_PER_DMA + sub;
+            const int lc = pc ^ L::swz(r);  // logical chunk it holds
+            const int64_t nrows = is_a ? M : N;
+            int64_t gr = (is_a ? m0 : n0) + r;
+            gr = gr < nrows ? gr : nrows - 1;
+            doff[D] = static_cast<unsigned>((gr * K + lc * 8) * 2);
+        });
+    }
+
+    template <int D>
+    __device__ __forceinline__ void issue_one(_Float16* stage, int64_t kt) const {
+        constexpr int op = op_of(D);
+        const _Float16* src = op == 0 ? A : (op == 1 ? W : (op == 2 ? Wlo : Alo));
+        constexpr int row = region_row(op) + round_of(D) * L::ROWS_PER_ROUND;
+        dma16_off(src + kt * BK, doff[D], stage + (row + wave * L::ROWS_PER_DMA) * BK);
+    }
+
+    // DMAs [LO, HI) of tile kt into `stage`.
+    template <int LO, int HI>
+    __device__ __forceinline__ void issue_range(_Float16* stage, int64_t kt) const {
+        static_for<LO, HI>([&](auto dd) { issue_one<decltype(dd)::value>(stage, kt); });
     }
 
     // Fragment of row `row` (tile-local), 16-wide k step `ks`: the 8 halves of
@@ -133,20 +168,29 @@ struct DmaGemm {
         return *reinterpret_cast<const half8*>(region + row * BK + pc * 8);
     }
 
-    __device__ __forceinline__ void compute(const _Float16* stage) {
-#pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
+    // Multiply the tile in `stage`; if `more`, issue tile kt_next into
+    // `next` meanwhile, one slice of its DMAs after each row of MFMAs, so the
+    // vector-memory issue (which stalls while the CU's load queue is full)
+    // runs under the matrix cores instead of ahead of them.
+    __device__ __forceinline__ void compute(const _Float16* stage, _Float16* next, int64_t kt_next,
+                                            bool more) {
+        constexpr int SLOTS = KS * TM;
+        static_for<0, KS>([&](auto kk) {
+            constexpr int ks = decltype(kk)::value;
             half8 a[TM], b[TN];
 #pragma unroll
             for (int i = 0; i < TM; ++i) a[i] = frag(stage + L::A_ROW * BK, wm * WM + i * 32 + lr, ks);
 #pragma unroll
             for (int j = 0; j < TN; ++j) b[j] = frag(stage + L::W_ROW * BK, wn * WN + j * 32 + lr, ks);
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
+            static_for<0, TM>([&](auto ii) {
+                constexpr int i = decltype(ii)::value;
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], a[i], acc[i][j], 0, 0, 0);
-            if constexpr (PASSES >= 2) {
+                constexpr int slot = ks * TM + i;
+                if (more) issue_range<slot * NDMA / SLOTS, (slot + 1) * NDMA / SLOTS>(next, kt_next);
+            });
+            if constexpr (L::SW) {
                 half8 bl[TN];
 #pragma unroll
                 for (int j = 0; j < TN; ++j) bl[j] = frag(stage + L::WLO_ROW * BK, wn * WN + j * 32 + lr, ks);
@@ -156,7 +200,7 @@ struct DmaGemm {
                     for (int j = 0; j < TN; ++j)
                         acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bl[j], a[i], acc2[i][j], 0, 0, 0);
             }
-            if constexpr (PASSES == 3) {
+            if constexpr (L::SA) {
                 half8 al[TM];
 #pragma unroll
                 for (int i = 0; i < TM; ++i) al[i] = frag(stage + L::ALO_ROW * BK, wm * WM + i * 32 + lr, ks);
@@ -166,7 +210,7 @@ struct DmaGemm {
                     for (int j = 0; j < TN; ++j)
                         acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], al[i], acc2[i][j], 0, 0, 0);
             }
-        }
+        });
     }
 
     // Wait until tile kt's DMAs (this wave's) have landed. Younger tiles
@@ -185,12 +229,12 @@ struct DmaGemm {
     }
 };
 
-template <int BM, int BN, int BK, int NS, int PASSES, int ACT, bool OUT_F16>
+template <int BM, int BN, int BK, int NS, int MODE, int ACT, bool OUT_F16>
 __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     const _Float16* __restrict__ A, const _Float16* __restrict__ Alo,
     const _Float16* __restrict__ W, const _Float16* __restrict__ Wlo,
     const float* __restrict__ bias, void* __restrict__ C, int64_t M, int64_t N, int64_t K) {
-    using G = DmaGemm<BM, BN, BK, NS, PASSES, ACT, OUT_F16>;
+    using G = DmaGemm<BM, BN, BK, NS, MODE, ACT, OUT_F16>;
     using L = typename G::L;
     static_assert(NS >= 2 && NS <= 8, "2 to 8 stages");
     static_assert((NS - 2) * L::LOADS < 64, "vmcnt is 6 bits");
@@ -220,12 +264,13 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     g.m0 = mt * BM;
     g.n0 = nt * BN;
     g.nk = K / BK;
+    g.init_offsets();
 #pragma unroll
     for (int i = 0; i < G::TM; ++i)
 #pragma unroll
         for (int j = 0; j < G::TN; ++j) {
             g.acc[i][j] = floatx16{};
-            if constexpr (PASSES > 1) g.acc2[i][j] = floatx16{};
+            if constexpr (G::SPLIT) g.acc2[i][j] = floatx16{};
         }
 
     auto stage = [&](auto s) -> _Float16* {
@@ -253,7 +298,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     auto prologue = [&](auto s) {
         constexpr int S = decltype(s)::value;
         if constexpr (S < NS - 1) {
-            if (S < g.nk) g.issue(stage(s), S);
+            if (S < g.nk) g.template issue_range<0, G::NDMA>(stage(s), S);
         }
     };
     prologue(std::integral_constant<int, 0>{});
@@ -266,15 +311,16 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
 
     // One step: wait for tile kt (in stage S), barrier (everyone's DMAs for kt
     // landed, everyone done reading the stage tile kt + NS - 1 will reuse),
-    // issue tile kt + NS - 1 into stage (S + NS - 1) % NS, multiply tile kt.
+    // multiply tile kt while issuing tile kt + NS - 1 into stage
+    // (S + NS - 1) % NS.
     auto step = [&](auto s, int64_t kt) {
         constexpr int S = decltype(s)::value;
         if constexpr (S < NS) {
             constexpr int NEXT = (S + NS - 1) % NS;
             g.wait_tile(kt);
             stage_barrier();
-            if (kt + NS - 1 < g.nk) g.issue(stage(std::integral_constant<int, NEXT>{}), kt + NS - 1);
-            g.compute(stage(s));
+            g.compute(stage(s), stage(std::integral_constant<int, NEXT>{}), kt + NS - 1,
+                      kt + NS - 1 < g.nk);
         }
     };
 
@@ -319,7 +365,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float a = g.acc[i][j][4 * grp + e];
-                    if constexpr (PASSES > 1) a += g.acc2[i][j][4 * grp + e] * kLoUnscale;
+                    if constexpr (G::SPLIT) a += g.acc2[i][j][4 * grp + e] * kLoUnscale;
                     a += sbias[cl + e];
                     if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
                     v[e] = a;
@@ -358,55 +404,77 @@ struct DmaArgs {
     hipStream_t stream;
 };
 
-template <int BM, int BN, int BK, int NS, int PASSES, int ACT, bool OUT_F16>
+template <int BM, int BN, int BK, int NS, int MODE, int ACT, bool OUT_F16>
 void launch_dma(const DmaArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, PASSES, ACT, OUT_F16>),
+    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, MODE, ACT, OUT_F16>),
                        dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, a.stream, a.A,
                        a.Alo, a.W, a.Wlo, a.bias, a.C, a.M, a.N, a.K);
 }
 
 // Tile ids (dotl_linear's `tile`): 0 128x128, 1 256x128, 2 64x64, 3 256x256,
 // 4 128x64. K tiles of 32; stage counts fill <= 144 KiB of LDS.
-template <int PASSES, int ACT, bool OUT_F16>
+template <int MODE, int ACT, bool OUT_F16>
 bool dispatch_tile(const DmaArgs& a, int tile) {
+    // Stage depths are chosen by operand planes a stage holds: 2 + split ones.
+    constexpr int PASSES = 1 + (MODE & 1) + ((MODE >> 1) & 1);
     switch (tile) {
         case 0:   // stage: 256 / 384 / 512 rows x 64 B = 16 / 24 / 32 KiB
-            if constexpr (PASSES == 1) launch_dma<128, 128, 32, 8, PASSES, ACT, OUT_F16>(a);
-            else if constexpr (PASSES == 2) launch_dma<128, 128, 32, 6, PASSES, ACT, OUT_F16>(a);
-            else launch_dma<128, 128, 32, 4, PASSES, ACT, OUT_F16>(a);
+            if constexpr (PASSES == 1) launch_dma<128, 128, 32, 8, MODE, ACT, OUT_F16>(a);
+            else if constexpr (PASSES == 2) launch_dma<128, 128, 32, 6, MODE, ACT, OUT_F16>(a);
+            else launch_dma<128, 128, 32, 4, MODE, ACT, OUT_F16>(a);
             return true;
         case 1:   // 384 rows: 24 KiB
-            if constexpr (PASSES == 1) { launch_dma<256, 128, 32, 6, PASSES, ACT, OUT_F16>(a); return true; }
+            if constexpr (PASSES == 1) { launch_dma<256, 128, 32, 6, MODE, ACT, OUT_F16>(a); return true; }
             return false;
         case 2:   // 128 / 192 / 256 rows
-            if constexpr (PASSES == 1) launch_dma<64, 64, 32, 8, PASSES, ACT, OUT_F16>(a);
-            else launch_dma<64, 64, 32, 8, PASSES, ACT, OUT_F16>(a);
+            if constexpr (PASSES == 1) launch_dma<64, 64, 32, 8, MODE, ACT, OUT_F16>(a);
+            else launch_dma<64, 64, 32, 8, MODE, ACT, OUT_F16>(a);
             return true;
         case 3:   // 512 rows: 32 KiB
-            if constexpr (PASSES == 1) { launch_dma<256, 256, 32, 4, PASSES, ACT, OUT_F16>(a); return true; }
+            if constexpr (PASSES == 1) { launch_dma<256, 256, 32, 4, MODE, ACT, OUT_F16>(a); return true; }
             return false;
         case 4:   // 192 / 320 / 384 rows
-            if constexpr (PASSES == 1) launch_dma<128, 64, 32, 8, PASSES, ACT, OUT_F16>(a);
-            else if constexpr (PASSES == 2) launch_dma<128, 64, 32, 7, PASSES, ACT, OUT_F16>(a);
-            else launch_dma<128, 64, 32, 6, PASSES, ACT, OUT_F16>(a);
+            if constexpr (PASSES == 1) launch_dma<128, 64, 32, 8, MODE, ACT, OUT_F16>(a);
+            else if constexpr (PASSES == 2) launch_dma<128, 64, 32, 7, MODE, ACT, OUT_F16>(a);
+            else launch_dma<128, 64, 32, 6, MODE, ACT, OUT_F16>(a);
             return true;
         // Shallow pipelines whose LDS (<= 72 KiB) lets two workgroups share a
         // CU, i.e. two waves per SIMD, the co-resident one hiding latency.
         case 5:
-            if constexpr (PASSES == 1) launch_dma<128, 128, 32, 4, PASSES, ACT, OUT_F16>(a);
-            else if constexpr (PASSES == 2) launch_dma<128, 128, 32, 3, PASSES, ACT, OUT_F16>(a);
-            else launch_dma<128, 128, 32, 2, PASSES, ACT, OUT_F16>(a);
+            if constexpr (PASSES == 1) launch_dma<128, 128, 32, 4, MODE, ACT, OUT_F16>(a);
+            else if constexpr (PASSES == 2) launch_dma<128, 128, 32, 3, MODE, ACT, OUT_F16>(a);
+            else launch_dma<128, 128, 32, 2, MODE, ACT, OUT_F16>(a);
             return true;
         case 6:
-            if constexpr (PASSES == 1) { launch_dma<256, 128, 32, 3, PASSES, ACT, OUT_F16>(a); return true; }
+            if constexpr (PASSES == 1) { launch_dma<256, 128, 32, 3, MODE, ACT, OUT_F16>(a); return true; }
             return false;
         case 7:
-            if constexpr (PASSES == 1) launch_dma<128, 64, 32, 4, PASSES, ACT, OUT_F16>(a);
-            else launch_dma<128, 64, 32, 3, PASSES, ACT, OUT_F16>(a);
+            if constexpr (PASSES == 1) launch_dma<128, 64, 32, 4, MODE, ACT, OUT_F16>(a);
+            else launch_dma<128, 64, 32, 3, MODE, ACT, OUT_F16>(a);
             return true;
         case 8:
-            launch_dma<64, 64, 32, 4, PASSES, ACT, OUT_F16>(a);
+            launch_dma<64, 64, 32, 4, MODE, ACT, OUT_F16>(a);
+            return true;
+        // BK = 64: each row of a stage is one whole 128-byte line, so every
+        // DMA instruction reads 8 full lines instead of 16 half lines.
+        case 9:   // 512 rows x 128 B = 64 KiB a stage
+            if constexpr (PASSES == 1) { launch_dma<256, 256, 64, 2, MODE, ACT, OUT_F16>(a); return true; }
+            return false;
+        case 10:  // 256 / 384 / 512 rows: 32 / 48 / 64 KiB
+            if constexpr (PASSES == 1) launch_dma<128, 128, 64, 4, MODE, ACT, OUT_F16>(a);
+            else if constexpr (PASSES == 2) launch_dma<128, 128, 64, 3, MODE, ACT, OUT_F16>(a);
+            else launch_dma<128, 128, 64, 2, MODE, ACT, OUT_F16>(a);
+            return true;
+        case 11:  // 384 rows: 48 KiB
+            if constexpr (PASSES == 1) { launch_dma<256, 128, 64, 3, MODE, ACT, OUT_F16>(a); return true; }
+            return false;
+        case 12:  // two workgroups a CU
+            if constexpr (PASSES == 1) { launch_dma<128, 128, 64, 2, MODE, ACT, OUT_F16>(a); return true; }
+            return false;
+        case 13:  // 192 / 320 / 384 rows
+            if constexpr (PASSES == 1) launch_dma<128, 64, 64, 3, MODE, ACT, OUT_F16>(a);
+            else launch_dma<128, 64, 64, 2, MODE, ACT, OUT_F16>(a);
             return true;
     }
     return false;
@@ -414,42 +482,43 @@ bool dispatch_tile(const DmaArgs& a, int tile) {
 
 }  // namespace
 
-// Tile choice, from sweeps of every GEMM of the five layer configs on MI355X:
-//   * one pass: 256x256 (deep pipeline, one workgroup per CU) for K >= 2048
-//     once it gives a workgroup per CU; otherwise the shallow-pipeline tiles,
-//     two or more workgroups per CU, the largest that still fills the CUs;
-//   * split (fp16x3) passes: the deep 128x128 pipeline for K >= 1024; for
-//     short K (256-512, a handful of K tiles) the shallow 128x128 when there
-//     are plenty of tiles, else 128x64.
+// Tile choice, from sweeps of every GEMM of the five layer configs on MI355X
+// (passes = planes multiplied: 1 + split x + split W):
+//   * one pass: 256x256 with 128-byte K rows for K >= 2048 once that gives a
+//     workgroup per CU; else the 128x128 two-stage tile (two workgroups a
+//     CU) when it fills the CUs four times over, or at short K; else
+//     128x64, then 64x64;
+//   * split passes: the 128x128 tile with 128-byte K rows when it fills the
+//     CUs, else the shallow 128x64, then 64x64.
 int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-    const int64_t fill = 240;
     if (passes == 1) {
-        if (K >= 2048 && tiles(256, 256) >= fill) return 3;
-        if (tiles(128, 128) >= fill) return 5;
-        if (tiles(128, 64) >= fill) return 7;
+        if (K >= 2048 && tiles(256, 256) >= 240) return 9;
+        if (tiles(128, 128) >= 960) return 12;
+        if (tiles(128, 128) >= 240 && K <= 1024) return 12;
+        if (tiles(128, 64) >= 200) return 13;
         return 8;
     }
-    if (K >= 1024 && tiles(128, 128) >= fill) return 0;
-    if (tiles(128, 128) >= 4 * fill) return 5;
-    if (tiles(128, 64) >= fill) return 7;
+    if (tiles(128, 128) >= 400) return 10;
+    if (tiles(128, 64) >= 240) return 7;
     return 8;
 }
 
 bool launch_gemm_dma(const _Float16* A, const _Float16* Alo, const _Float16* W,
                      const _Float16* Wlo, const float* bias, void* C, int64_t M, int64_t N,
-                     int64_t K, int passes, int act, bool out_f16, int tile, hipStream_t stream) {
+                     int64_t K, int mode, int act, bool out_f16, int tile, hipStream_t stream) {
     const DmaArgs a{A, Alo, W, Wlo, bias, C, M, N, K, stream};
-    auto by_out = [&](auto p) {
-        constexpr int P = decltype(p)::value;
+    auto by_out = [&](auto m) {
+        constexpr int MD = decltype(m)::value;
         if (act == DOTL_ACT_GELU) {
-            return out_f16 ? dispatch_tile<P, DOTL_ACT_GELU, true>(a, tile)
-                           : dispatch_tile<P, DOTL_ACT_GELU, false>(a, tile);
+            return out_f16 ? dispatch_tile<MD, DOTL_ACT_GELU, true>(a, tile)
+                           : dispatch_tile<MD, DOTL_ACT_GELU, false>(a, tile);
         }
-        return out_f16 ? dispatch_tile<P, DOTL_ACT_NONE, true>(a, tile)
-                       : dispatch_tile<P, DOTL_ACT_NONE, false>(a, tile);
+        return out_f16 ? dispatch_tile<MD, DOTL_ACT_NONE, true>(a, tile)
+                       : dispatch_tile<MD, DOTL_ACT_NONE, false>(a, tile);
     };
-    switch (passes) {
+    switch (mode) {
+        case 0: return by_out(std::integral_constant<int, 0>{});
         case 1: return by_out(std::integral_constant<int, 1>{});
         case 2: return by_out(std::integral_constant<int, 2>{});
         case 3: return by_out(std::integral_constant<int, 3>{});

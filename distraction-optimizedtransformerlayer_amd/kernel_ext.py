@@ -48,6 +48,7 @@ DOTL_ACT_NONE = 0
 DOTL_ACT_GELU = 1
 DOTL_MATH_FP16 = 0
 DOTL_MATH_FP16X3 = 1
+DOTL_MATH_FP16X2 = 2
 
 # Every symbol include/dotl.h declares.
 EXPORTED_SYMBOLS = (
@@ -413,10 +414,13 @@ class Kernels:
             return None
         return out
 
-    def linear_bias_split(self, planes, weight, bias, tile=-1, out_half=False):
+    def linear_bias_split(self, planes, weight, bias, tile=-1, out_half=False,
+                          split_weight=True):
         """x @ weight^T + bias with x given as split fp16 planes [2, ..., K]
-        (fused_layernorm_split's output), in the fp16x3 arithmetic: three MFMA
-        passes, fp32-class products. Not in the reference's surface.
+        (fused_layernorm_split's output). split_weight=True: the fp16x3
+        arithmetic, three MFMA passes, fp32-class products; False: fp16x2,
+        hi(x)*W + lo(x)*W with W in fp16, two passes. Not in the reference's
+        surface.
         """
         import torch
 
@@ -430,13 +434,14 @@ class Kernels:
         K, N = weight.shape[1], weight.shape[0]
         pc = planes.contiguous()
         M = pc[0].numel() // K
-        hi, lo = self.weight_half(weight, True)
+        hi, lo = self.weight_half(weight, bool(split_weight))
         out = torch.empty((*pc.shape[1:-1], N), dtype=torch.float16 if out_half else torch.float32,
                           device=pc.device)
         rc = self._check(self._lib.dotl_linear(
-            pc.data_ptr(), DOTL_F16X2, hi.data_ptr(), lo.data_ptr(), bias.contiguous().data_ptr(),
-            out.data_ptr(), DOTL_F16 if out_half else DOTL_F32, M, N, K, DOTL_ACT_NONE,
-            DOTL_MATH_FP16X3, int(tile), self._stream(pc.device)))
+            pc.data_ptr(), DOTL_F16X2, hi.data_ptr(), lo.data_ptr() if lo is not None else None,
+            bias.contiguous().data_ptr(), out.data_ptr(), DOTL_F16 if out_half else DOTL_F32,
+            M, N, K, DOTL_ACT_NONE, DOTL_MATH_FP16X3 if split_weight else DOTL_MATH_FP16X2,
+            int(tile), self._stream(pc.device)))
         if rc == DOTL_DECLINED:
             return None
         return out

@@ -94,11 +94,12 @@ def _split_planes(t: torch.Tensor) -> torch.Tensor:
 def _normed_split_wanted() -> bool:
     """Should a LayerNorm feeding the QKV projection emit split fp16 planes?
 
-    Yes exactly when that projection runs the fp16x3 arithmetic on the
-    pipelined GEMM: the planes carry ~22 bits of the LayerNorm output in the
-    same bytes as fp32, already in the form the three MFMA passes read.
+    Yes exactly when that projection runs a split arithmetic (fp16x2 or
+    fp16x3) on the pipelined GEMM: the planes carry ~22 bits of the LayerNorm
+    output in the same bytes as fp32, already in the form the MFMA passes
+    read.
     """
-    return (config.LINEAR_BIAS == "auto" and config.QKV_PRECISION == "fp16x3"
+    return (config.LINEAR_BIAS == "auto" and config.QKV_PRECISION in ("fp16x3", "fp16x2")
             and config.NORMED_FP16 != "off")
 
 
@@ -124,10 +125,11 @@ def _add_layernorm_split(x: torch.Tensor, sub: torch.Tensor, norm):
 
 def _linear_bias_split(planes: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
                        out_half: bool = False) -> torch.Tensor:
-    """planes-as-x @ weight^T + bias in the fp16x3 arithmetic."""
+    """planes-as-x @ weight^T + bias in the split arithmetic config.QKV_PRECISION names."""
     kernels = _custom_kernels()
     if kernels is not None:
-        out = kernels.linear_bias_split(planes, weight, bias, -1, out_half)
+        out = kernels.linear_bias_split(planes, weight, bias, -1, out_half,
+                                        split_weight=config.QKV_PRECISION == "fp16x3")
         if out is not None:
             return out
     fallback_counts["linear_bias"] += 1

@@ -58,6 +58,8 @@ extern "C" {
 #define DOTL_MATH_FP16 0   /* fp16 operands, fp32 accumulate: one MFMA pass */
 #define DOTL_MATH_FP16X3 1 /* split fp16 hi+lo operands, three MFMA passes:
                               fp32-class products (the reference's tf32 slot) */
+#define DOTL_MATH_FP16X2 2 /* x as split fp16 hi+lo planes, W in fp16: two
+                              passes, hi(x)*W + 2^-12 lo(x)*W */
 
 /* Thread-local message for the last negative return; "" if none. */
 const char* dotl_last_error(void);
@@ -130,14 +132,17 @@ int dotl_weight_split(const float* w, void* w_hi, void* w_lo, int64_t n, void* s
  *   bias      [N] float32 (required; the reference's kernels always add one)
  *   out       [M, N], out_dtype DOTL_F32 or DOTL_F16 (RNE)
  *   act       DOTL_ACT_NONE / DOTL_ACT_GELU, applied in fp32 before the store
- *   math      DOTL_MATH_FP16 or DOTL_MATH_FP16X3 (an fp16 x is exact in
+ *   math      DOTL_MATH_FP16, DOTL_MATH_FP16X3 (an fp16 x is exact in
  *             fp16, so with it the split path runs two passes: x*hi + x*lo;
- *             a DOTL_F16X2 x runs three: + lo(x)*hi(W))
+ *             a DOTL_F16X2 x runs three: + lo(x)*hi(W)) or DOTL_MATH_FP16X2
+ *             (DOTL_F16X2 x only; w_lo unused)
  *   tile      -1 auto; otherwise a tile id (0: 128x128, 1: 256x128 [one
  *             pass], 2: 64x64, 3: 256x256 [one pass], 4: 128x64; 5-8: 128x128,
  *             256x128 [one pass], 128x64, 64x64 with shallower pipelines that
- *             fit two workgroups per CU); 100 + id (id <= 4) forces the
- *             register-staged kernel (for measurement)
+ *             fit two workgroups per CU; 9-13: 256x256 [one pass], 128x128,
+ *             256x128 [one pass], 128x128 [one pass, two stages], 128x64 with
+ *             128-byte K rows); 100 + id (id <= 4) forces the register-staged
+ *             kernel (for measurement)
  *   fp16 / split-fp16 x with K % 64 == 0 runs the LDS-DMA pipelined kernel;
  *   anything else the register-staged one. Declines when K % 8 != 0, or a
  *   DOTL_F16X2 x with K % 64 != 0.

@@ -58,6 +58,12 @@ def test_linear_rejects_bad_codes(lib):
     assert lib.dotl_linear(None, 0, None, None, None, None, 0, 4, 4, 16, 5, 0, -1, None) == -1
     # fp16x3 without the weight residual
     assert lib.dotl_linear(None, 0, None, None, None, None, 0, 4, 4, 16, 0, 1, -1, None) == -1
+    # fp16x2 (split x only) takes x as split planes (dtype 2), nothing else
+    assert lib.dotl_linear(None, 1, None, None, None, None, 0, 4, 4, 64, 0, 2, -1, None) == -1
+    assert b"split fp16 planes" in lib.dotl_last_error()
+    assert lib.dotl_linear(None, 2, None, None, None, None, 0, 0, 4, 64, 0, 2, -1, None) == 0
+    # tile ids beyond the menu
+    assert lib.dotl_linear(None, 1, None, None, None, None, 0, 4, 4, 64, 0, 0, 14, None) == -1
     # empty problems launch nothing and succeed
     assert lib.dotl_linear(None, 0, None, None, None, None, 0, 0, 4, 16, 0, 0, -1, None) == 0
 

@@ -368,8 +368,12 @@ def test_layernorm_split_planes(kernels, rows, D):
 DMA_SHAPES = [(300, 200, 128), (1000, 1024, 256), (64, 2048, 512), (513, 384, 64)]
 
 
+ALL_TILES = [-1] + list(range(14))
+SPLIT_TILES = [-1, 0, 2, 4, 5, 7, 8, 10, 13]   # the tiles built for split passes
+
+
 @pytest.mark.parametrize("M,N,K", DMA_SHAPES)
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 4])
+@pytest.mark.parametrize("tile", ALL_TILES)
 def test_gemm_dma_one_pass(kernels, M, N, K, tile):
     """fp16 x on the pipelined kernel: every tile, with M and N tails."""
     x, w, b = _gemm_case(M, N, K, 7 * M + N)
@@ -377,12 +381,12 @@ def test_gemm_dma_one_pass(kernels, M, N, K, tile):
     got = kernels.linear_bias(_t(x).half(), _t(w), _t(b), tile, -1).cpu().numpy()
     np.testing.assert_allclose(got, want, atol=2e-5 * np.sqrt(K / 128), rtol=1e-5)
     # the register-staged kernel (tile 100 + id) gives the same numbers
-    staged = kernels.linear_bias(_t(x).half(), _t(w), _t(b), 100 + max(tile, 0), -1)
+    staged = kernels.linear_bias(_t(x).half(), _t(w), _t(b), 100 + (tile if 0 <= tile <= 4 else 0), -1)
     np.testing.assert_allclose(got, staged.cpu().numpy(), atol=2e-5 * np.sqrt(K / 128))
 
 
 @pytest.mark.parametrize("M,N,K", DMA_SHAPES)
-@pytest.mark.parametrize("tile", [-1, 0, 2, 4])
+@pytest.mark.parametrize("tile", SPLIT_TILES)
 def test_gemm_dma_split_weight(kernels, M, N, K, tile):
     """fp16 x with the fp16x3 math: two passes, x * (hi + 2^-12 lo) of the fp32 W."""
     x, w, b = _gemm_case(M, N, K, 5 * M + N)
@@ -392,7 +396,26 @@ def test_gemm_dma_split_weight(kernels, M, N, K, tile):
 
 
 @pytest.mark.parametrize("M,N,K", DMA_SHAPES)
-@pytest.mark.parametrize("tile", [-1, 0, 2, 4])
+@pytest.mark.parametrize("tile", SPLIT_TILES)
+def test_gemm_dma_split_x_only(kernels, M, N, K, tile):
+    """Split-plane x with an fp16 W (the fp16x2 arithmetic): two passes,
+    (hi + 2^-12 lo)(x) * fp16(W), against the fp64 GEMM of those operands."""
+    x, w, b = _gemm_case(M, N, K, 11 * M + N)
+    xt = _t(x)
+    hi = xt.half()
+    lo = ((xt - hi.float()) * 4096.0).half()
+    planes = torch.stack([hi, lo])
+    xr = hi.double().cpu().numpy() + lo.double().cpu().numpy() / 4096.0
+    want = xr @ _h(w).T + b
+    got = kernels.linear_bias_split(planes, _t(w), _t(b), tile, False, split_weight=False)
+    np.testing.assert_allclose(got.cpu().numpy(), want, atol=3e-6 * np.sqrt(K / 128), rtol=2e-6)
+    # and it differs from the three-pass arithmetic by W's fp16 rounding
+    three = kernels.linear_bias_split(planes, _t(w), _t(b), tile, False).cpu().numpy()
+    assert np.abs(three - got.cpu().numpy()).max() > 1e-5
+
+
+@pytest.mark.parametrize("M,N,K", DMA_SHAPES)
+@pytest.mark.parametrize("tile", SPLIT_TILES)
 @pytest.mark.parametrize("act", ["none", "half_out"])
 def test_gemm_dma_split_planes(kernels, M, N, K, tile, act):
     """Split-plane x: three passes, fp32-class products against the fp64 GEMM."""
