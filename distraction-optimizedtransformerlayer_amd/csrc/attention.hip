@@ -563,9 +563,12 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
     p.causal = is_causal ? 1 : 0;
     int nw = waves_for(S), ns = 0;
     if (dtype == DOTL_F16 && attention_cp_async_mode() != 0) {
+        // The pipelined kernel: 8 waves (256 queries) a workgroup for
+        // head_dim 128 from S = 2048, measured 4% faster there than 4.
+        if (head_dim == 128 && S >= 2048) nw = 8;
         int fnw = 0, fns = 0;
         attention_pipeline(&fnw, &fns);
-        if (fnw == 1 || fnw == 2 || fnw == 4) nw = fnw;
+        if (fnw == 1 || fnw == 2 || fnw == 4 || fnw == 8) nw = fnw;
         if (fns >= 1 && fns <= 4) ns = fns;
     }
     p.nqb = use_scalar ? attn_scalar_query_blocks(S, head_dim) : (S + 32 * nw - 1) / (32 * nw);

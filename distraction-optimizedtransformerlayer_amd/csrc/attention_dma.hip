@@ -73,7 +73,7 @@ __device__ __forceinline__ half4 lds_read_tr(const _Float16* p) {
 }
 
 template <int HD, int NW, int NS, bool OUT_F32>
-__global__ __launch_bounds__(NW * 64, 2) void attn_dma_kernel(AttnParams p) {
+__global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(AttnParams p) {
     using TL = AttnTile<HD>;
     constexpr int KS = HD / 16;            // k-steps of the score product
     constexpr int HT = HD / 32;            // 32-row hd tiles of O^T
@@ -603,18 +603,21 @@ void launch_nw(const AttnParams& p, int nw, hipStream_t stream) {
     switch (nw) {
         case 1: launch_capped<HD, 1, NS, OUT_F32>(p, stream); break;
         case 2: launch_capped<HD, 2, NS, OUT_F32>(p, stream); break;
+        case 8: launch_capped<HD, 8, NS, OUT_F32>(p, stream); break;
         default: launch_capped<HD, 4, NS, OUT_F32>(p, stream); break;
     }
 }
 
 // Pipeline depth: 2 stages (one tile in flight while one is multiplied),
 // one when a head_dim <= 64 sequence is a single tile. Measured on MI355X at
-// the layer configs, 2 stages beat 3 and 4: at 2 waves per SIMD the
-// co-resident workgroup hides the load latency, and deeper pipelines cost
-// LDS, hence workgroups per CU.
+// the layer configs, 2 stages beat 3 and 4 at 4 waves a workgroup: at 2
+// waves per SIMD the co-resident workgroup hides the load latency, and
+// deeper pipelines cost LDS, hence workgroups per CU. The exception is the
+// 8-wave workgroup (head_dim 128, long sequences): one workgroup a CU, so
+// its own third stage hides the latency.
 template <int HD, bool OUT_F32>
 void launch_ns(const AttnParams& p, int nw, int ns, hipStream_t stream) {
-    if (ns <= 0) ns = (HD < 128 && p.S <= kKB) ? 1 : 2;
+    if (ns <= 0) ns = nw == 8 ? 3 : ((HD < 128 && p.S <= kKB) ? 1 : 2);
     switch (ns) {
         case 1: launch_nw<HD, 1, OUT_F32>(p, nw, stream); break;
         case 2: launch_nw<HD, 2, OUT_F32>(p, nw, stream); break;

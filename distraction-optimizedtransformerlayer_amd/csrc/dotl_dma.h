@@ -61,8 +61,19 @@ __device__ __forceinline__ void dma16(const void* g, const void* lds) {
 }
 
 // The same load addressed as a wave-uniform 64-bit base (SGPRs) plus this
-// lane's 32-bit byte offset: no per-lane 64-bit address arithmetic.
-__device__ __forceinline__ void dma16_off(const void* base, unsigned offset, const void* lds) {
+// lane's 32-bit byte offset: no per-lane 64-bit address arithmetic. The
+// base is uniform by contract; readfirstlane states it where the compiler
+// cannot prove it (an "s" operand it has placed in VGPRs does not assemble).
+__device__ __forceinline__ void dma16_off(const void* base_any, unsigned offset, const void* lds) {
+    // readfirstlane returns a signed int: each word goes through unsigned
+    // before widening, or a low word >= 2^31 would sign-extend into the high
+    // one.
+    const uint64_t b64 = reinterpret_cast<uintptr_t>(base_any);
+    const uint64_t lo = static_cast<unsigned>(
+        __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<unsigned>(b64))));
+    const uint64_t hi = static_cast<unsigned>(
+        __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<unsigned>(b64 >> 32))));
+    const void* base = reinterpret_cast<const void*>(lo | (hi << 32));
     const unsigned lbase = lds_offset(lds);
     unsigned saved;
     asm volatile(

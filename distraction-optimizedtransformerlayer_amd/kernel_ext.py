@@ -605,7 +605,7 @@ class Kernels:
         self._lib.dotl_wmma_set_cp_async(int(mode))
 
     def attention_set_pipeline(self, waves: int = 0, stages: int = 0) -> None:
-        """Force the LDS-DMA attention kernel's waves per workgroup (1, 2, 4)
+        """Force the LDS-DMA attention kernel's waves per workgroup (1, 2, 4, 8)
         and pipeline stages (1-4); 0 restores the automatic choice.
         A measurement knob; not in the reference's surface."""
         self._lib.dotl_attention_set_pipeline(int(waves), int(stages))

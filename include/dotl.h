@@ -230,8 +230,9 @@ void dotl_wmma_set_cp_async(int mode);
 int dotl_wmma_cp_async_mode(void);
 
 /* Measurement knob of the LDS-DMA attention kernel, no reference
- * counterpart: force its wavefronts per workgroup (1, 2 or 4; 0 = by
- * sequence length) and pipeline stages (1 to 4; 0 = by head_dim and length).
+ * counterpart: force its wavefronts per workgroup (1, 2, 4 or 8; 0 = by
+ * sequence length and head_dim) and pipeline stages (1 to 4; 0 = by
+ * head_dim, length and waves).
  * Process-wide, like the knobs above. */
 void dotl_attention_set_pipeline(int waves, int stages);
 
