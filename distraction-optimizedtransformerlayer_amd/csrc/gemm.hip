@@ -38,8 +38,9 @@ namespace dotl {
 
 int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes);
 bool launch_gemm_dma(const _Float16* A, const _Float16* Alo, const _Float16* W,
-                     const _Float16* Wlo, const float* bias, void* C, int64_t M, int64_t N,
-                     int64_t K, int mode, int act, bool out_f16, int tile, hipStream_t stream);
+                     const _Float16* Wlo, const float* bias, const float* R, void* C, int64_t M,
+                     int64_t N, int64_t K, int mode, int act, bool out_f16, int tile,
+                     hipStream_t stream);
 
 namespace {
 
@@ -429,10 +430,12 @@ extern "C" int dotl_weight_split(const float* w, void* w_hi, void* w_lo, int64_t
     return check_launch("weight_split");
 }
 
-extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
-                           const float* bias, void* out, int out_dtype, int64_t M, int64_t N,
-                           int64_t K, int act, int math, int tile, void* stream) {
-    using namespace dotl;
+namespace dotl {
+namespace {
+
+int linear_impl(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
+                const float* bias, const float* residual, void* out, int out_dtype, int64_t M,
+                int64_t N, int64_t K, int act, int math, int tile, void* stream) {
     clear_error();
     const char* who = act == DOTL_ACT_GELU ? "linear_gelu" : "linear_bias";
     DOTL_REQUIRE(x_dtype == DOTL_F32 || x_dtype == DOTL_F16 || x_dtype == DOTL_F16X2,
@@ -478,8 +481,8 @@ extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const v
         const int passes = 1 + (mode & 1) + ((mode >> 1) & 1);
         const int t = tile < 0 ? pick_dma_tile(M, N, K, passes) : tile;
         if (launch_gemm_dma(xh, xl, static_cast<const _Float16*>(w_hi),
-                            static_cast<const _Float16*>(w_lo), bias, out, M, N, K, mode, act,
-                            of16, t, as_stream(stream))) {
+                            static_cast<const _Float16*>(w_lo), bias, residual, out, M, N, K,
+                            mode, act, of16, t, as_stream(stream))) {
             return check_launch(who);
         }
         DOTL_REQUIRE(x_dtype != DOTL_F16X2, "%s: tile id %d is not built for split passes", who, tile);
@@ -487,6 +490,11 @@ extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const v
     DOTL_REQUIRE(x_dtype != DOTL_F16X2,
                  "%s: split-fp16 x is served by the pipelined kernel only (K %% 64 == 0, operands "
                  "under 4 GiB)", who);
+    if (residual != nullptr) {
+        set_error(std::string(who) + ": the residual epilogue is served by the pipelined kernel "
+                  "only (fp16 or split x, K % 64 == 0); add the residual separately");
+        return DOTL_DECLINED;
+    }
 
     GemmArgs g{x, static_cast<const _Float16*>(w_hi), static_cast<const _Float16*>(w_lo), bias,
                out, M, N, K, as_stream(stream)};
@@ -502,4 +510,27 @@ extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const v
     }
     DOTL_REQUIRE(ok, "%s: tile id %d is not built for these operand types", who, tile);
     return check_launch(who);
+}
+
+}  // namespace
+}  // namespace dotl
+
+extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
+                           const float* bias, void* out, int out_dtype, int64_t M, int64_t N,
+                           int64_t K, int act, int math, int tile, void* stream) {
+    return dotl::linear_impl(x, x_dtype, w_hi, w_lo, bias, nullptr, out, out_dtype, M, N, K, act,
+                             math, tile, stream);
+}
+
+extern "C" int dotl_linear_residual(const void* x, int x_dtype, const void* w_hi,
+                                    const void* w_lo, const float* bias, const float* residual,
+                                    float* out, int64_t M, int64_t N, int64_t K, int act, int math,
+                                    int tile, void* stream) {
+    using namespace dotl;
+    clear_error();
+    DOTL_REQUIRE(M == 0 || N == 0 || residual != nullptr, "linear_bias: null residual");
+    DOTL_REQUIRE(reinterpret_cast<uintptr_t>(residual) % 16 == 0,
+                 "linear_bias: the residual must be 16-byte aligned");
+    return linear_impl(x, x_dtype, w_hi, w_lo, bias, residual, out, DOTL_F32, M, N, K, act, math,
+                       tile, stream);
 }

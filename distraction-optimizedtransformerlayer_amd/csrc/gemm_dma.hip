@@ -233,7 +233,8 @@ template <int BM, int BN, int BK, int NS, int MODE, int ACT, bool OUT_F16>
 __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     const _Float16* __restrict__ A, const _Float16* __restrict__ Alo,
     const _Float16* __restrict__ W, const _Float16* __restrict__ Wlo,
-    const float* __restrict__ bias, void* __restrict__ C, int64_t M, int64_t N, int64_t K) {
+    const float* __restrict__ bias, const float* __restrict__ R, void* __restrict__ C, int64_t M,
+    int64_t N, int64_t K) {
     using G = DmaGemm<BM, BN, BK, NS, MODE, ACT, OUT_F16>;
     using L = typename G::L;
     static_assert(NS >= 2 && NS <= 8, "2 to 8 stages");
@@ -370,6 +371,22 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
                     if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
                     v[e] = a;
                 }
+                if constexpr (!OUT_F16) {
+                    // residual stream: out = R + act(x W^T + b), the add the
+                    // following LayerNorm would otherwise do (same fp32 sum)
+                    if (R != nullptr) {
+                        const float* rrow = R + row * N + col;
+                        if (vec_ok && col + 4 <= N) {
+                            const float4 r4 = *reinterpret_cast<const float4*>(rrow);
+                            v[0] = r4.x + v[0]; v[1] = r4.y + v[1];
+                            v[2] = r4.z + v[2]; v[3] = r4.w + v[3];
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (col + e < N) v[e] = rrow[e] + v[e];
+                        }
+                    }
+                }
                 if (vec_ok && col + 4 <= N) {
                     if constexpr (OUT_F16) {
                         half4 h;
@@ -399,6 +416,7 @@ struct DmaArgs {
     const _Float16* W;
     const _Float16* Wlo;
     const float* bias;
+    const float* R;      // nullable fp32 [M, N] residual added to an fp32 output
     void* C;
     int64_t M, N, K;
     hipStream_t stream;
@@ -409,7 +427,7 @@ void launch_dma(const DmaArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, MODE, ACT, OUT_F16>),
                        dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, a.stream, a.A,
-                       a.Alo, a.W, a.Wlo, a.bias, a.C, a.M, a.N, a.K);
+                       a.Alo, a.W, a.Wlo, a.bias, a.R, a.C, a.M, a.N, a.K);
 }
 
 // Tile ids (dotl_linear's `tile`): 0 128x128, 1 256x128, 2 64x64, 3 256x256,
@@ -505,9 +523,10 @@ int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
 }
 
 bool launch_gemm_dma(const _Float16* A, const _Float16* Alo, const _Float16* W,
-                     const _Float16* Wlo, const float* bias, void* C, int64_t M, int64_t N,
-                     int64_t K, int mode, int act, bool out_f16, int tile, hipStream_t stream) {
-    const DmaArgs a{A, Alo, W, Wlo, bias, C, M, N, K, stream};
+                     const _Float16* Wlo, const float* bias, const float* R, void* C, int64_t M,
+                     int64_t N, int64_t K, int mode, int act, bool out_f16, int tile,
+                     hipStream_t stream) {
+    const DmaArgs a{A, Alo, W, Wlo, bias, R, C, M, N, K, stream};
     auto by_out = [&](auto m) {
         constexpr int MD = decltype(m)::value;
         if (act == DOTL_ACT_GELU) {

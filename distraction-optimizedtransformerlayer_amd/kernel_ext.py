@@ -56,7 +56,7 @@ EXPORTED_SYMBOLS = (
     "dotl_mfma_layout_probe", "dotl_layernorm", "dotl_weight_split", "dotl_linear",
     "dotl_attention_forward", "dotl_ffn_block", "dotl_wmma_set_fp16", "dotl_wmma_fp16",
     "dotl_wmma_set_cp_async", "dotl_wmma_cp_async_mode", "dotl_lds_dma_probe",
-    "dotl_attention_set_pipeline",
+    "dotl_attention_set_pipeline", "dotl_linear_residual",
 )
 
 _kernels = None
@@ -105,6 +105,9 @@ def _declare(lib) -> None:
     lib.dotl_weight_split.argtypes = [vp, vp, vp, i64, vp]
     lib.dotl_linear.restype = i32
     lib.dotl_linear.argtypes = [vp, i32, vp, vp, vp, vp, i32, i64, i64, i64, i32, i32, i32, vp]
+    lib.dotl_linear_residual.restype = i32
+    lib.dotl_linear_residual.argtypes = [vp, i32, vp, vp, vp, vp, vp, i64, i64, i64, i32, i32,
+                                         i32, vp]
     lib.dotl_attention_forward.restype = i32
     lib.dotl_attention_forward.argtypes = [vp, vp, vp, i32, c.POINTER(i64), vp, c.POINTER(i64),
                                            vp, i32, i32, i32, i32, i32, i32, i32, c.c_double,
@@ -380,7 +383,7 @@ class Kernels:
                     out.append(lo)
         return out
 
-    def _gemm(self, who, x, weight, bias, tile, math, act, out_half):
+    def _gemm(self, who, x, weight, bias, tile, math, act, out_half, residual=None):
         import torch
 
         self._require_cuda(who, x, weight, bias)
@@ -406,10 +409,20 @@ class Kernels:
         bc = bias.contiguous()
         out = torch.empty((*xc.shape[:-1], N), dtype=torch.float16 if out_half else torch.float32,
                           device=xc.device)
-        rc = self._check(self._lib.dotl_linear(
-            xc.data_ptr(), xcode, hi.data_ptr(), lo.data_ptr() if lo is not None else None,
-            bc.data_ptr(), out.data_ptr(), DOTL_F16 if out_half else DOTL_F32, M, N, K, act, m,
-            int(tile), self._stream(x.device)))
+        if residual is not None:
+            if out_half or residual.dtype != torch.float32 or tuple(residual.shape) != tuple(out.shape):
+                raise RuntimeError(f"{who}: residual must be float32 with the output's shape "
+                                   f"{tuple(out.shape)}, and the output float32")
+            rc_ = residual.contiguous()
+            rc = self._check(self._lib.dotl_linear_residual(
+                xc.data_ptr(), xcode, hi.data_ptr(), lo.data_ptr() if lo is not None else None,
+                bc.data_ptr(), rc_.data_ptr(), out.data_ptr(), M, N, K, act, m, int(tile),
+                self._stream(x.device)))
+        else:
+            rc = self._check(self._lib.dotl_linear(
+                xc.data_ptr(), xcode, hi.data_ptr(), lo.data_ptr() if lo is not None else None,
+                bc.data_ptr(), out.data_ptr(), DOTL_F16 if out_half else DOTL_F32, M, N, K, act,
+                m, int(tile), self._stream(x.device)))
         if rc == DOTL_DECLINED:
             return None
         return out
@@ -446,9 +459,15 @@ class Kernels:
             return None
         return out
 
-    def linear_bias(self, x, weight, bias, tile=-1, math=-1, out_half=False):
-        """x @ weight^T + bias, or None when the shape/dtype is not covered."""
-        return self._gemm("linear_bias", x, weight, bias, tile, math, DOTL_ACT_NONE, out_half)
+    def linear_bias(self, x, weight, bias, tile=-1, math=-1, out_half=False, residual=None):
+        """x @ weight^T + bias, or None when the shape/dtype is not covered.
+
+        `residual` (not in the reference's signature; appended, default None):
+        an fp32 tensor of the output's shape added in the epilogue, the
+        residual add of the add+LayerNorm that follows out_proj / ffn_out.
+        """
+        return self._gemm("linear_bias", x, weight, bias, tile, math, DOTL_ACT_NONE, out_half,
+                          residual)
 
     def linear_gelu(self, x, weight, bias, tile=-1, math=-1, out_half=False):
         """GELU_erf(x @ weight^T + bias), or None when not covered.

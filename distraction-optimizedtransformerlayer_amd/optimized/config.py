@@ -6,10 +6,11 @@ through the module (`config.CUDA_GRAPH = "off"`): a `from ... import` binds
 the value, not the setting. The thresholds below were re-derived for MI355X
 (256 CUs, 288 GB HBM3E) rather than carried over from the reference's card.
 
-Three knobs are new in this build:
+Five knobs are new in this build:
   QKV_PRECISION  arithmetic of the fused QKV projection (fp16x2, fp16x3, fp16)
   GELU_FP16      whether linear_gelu stores its output as fp16 for ffn_out
   ROW_PACKING    whether a padded batch runs on its valid rows only
+  RESIDUAL_EPILOGUE  whether out_proj and ffn_out add the residual stream
 """
 
 # Attention backend. One legal value: the custom kernels, never a prebuilt
@@ -138,6 +139,17 @@ _GRAPH_SEED = 20240827
 # zeroes the padded ones with masked_fill, as the reference does. Same
 # outputs either way (bit-identical on prefix masks); see optimized/packing.py.
 ROW_PACKING = "auto"
+
+# Residual adds in the GEMM epilogue: "auto" makes out_proj write x + attn
+# and ffn_out write h1 + ffn (the same fp32 sums, bit-identical outputs), so
+# the LayerNorms after them read one tensor and write only the normalised
+# one; "off" keeps the reference's add+LayerNorm kernels. "auto" applies
+# from d_model _RESIDUAL_EPILOGUE_MIN_D: the epilogue's residual reads cost
+# more than the LayerNorm traffic they save when K is short. Same-box A/B
+# (layer µs, on / off): C3 307 / 312, C4 1446 / 1460; C1 42.3 / 40.7,
+# C2 120.7 / 119.2, C5 627 / 622.
+RESIDUAL_EPILOGUE = "auto"
+_RESIDUAL_EPILOGUE_MIN_D = 1024
 
 # Split the batch and retry when a forward runs out of memory.
 MICROBATCH_FALLBACK = True

@@ -80,7 +80,7 @@ def _graph_key(x: torch.Tensor, use_mask: bool, packing=None) -> Tuple:
     """Everything a capture freezes: shape/dtype/device, mask mode (and the
     packed row count, which sizes the packed path's GEMMs) and the knobs."""
     return (tuple(x.shape), x.dtype, x.device.index, use_mask,
-            None if packing is None else packing.key(), config.ROW_PACKING,
+            None if packing is None else packing.key(), config.ROW_PACKING, config.RESIDUAL_EPILOGUE,
             config.ATTENTION_IMPL, config.LINEAR_GELU, config.LINEAR_BIAS, config.LAYERNORM,
             config.QKV_FP16, config.NORMED_FP16, config.CP_ASYNC, config.ATTENTION_PRECISION,
             config.QKV_PRECISION, config.GELU_FP16)

@@ -185,6 +185,24 @@ def _add_layernorm_unpack(x: torch.Tensor, sub: torch.Tensor, norm, packing) -> 
     return out.view(shape)
 
 
+def _layernorm_unpack(x: torch.Tensor, norm, packing) -> torch.Tensor:
+    """LayerNorm of packed rows, returned as [B, S, D] with zero padded rows:
+    the model's output norm and the reference's final masked_fill in one
+    kernel (the scatter back from packed rows)."""
+    width = x.shape[-1]
+    shape = (packing.batch, packing.seq_len, width)
+    kernels = _custom_kernels()
+    if kernels is not None:
+        _, out = kernels.fused_layernorm_rows(x, norm.weight, norm.bias, packing.inv, norm.eps,
+                                              "float", False)
+        return out.view(shape)
+    fallback_counts["layernorm"] += 1
+    y = F.layer_norm(x, (width,), norm.weight, norm.bias, norm.eps)
+    out = torch.zeros(packing.batch * packing.seq_len, width, dtype=y.dtype, device=y.device)
+    out.index_copy_(0, packing.idx.long(), y)
+    return out.view(shape)
+
+
 def _layernorm(x: torch.Tensor, norm, out_half: bool = False) -> torch.Tensor:
     """LayerNorm(x) * w + b: the model's one norm with no residual before it."""
     if config.LAYERNORM != "off":
@@ -244,21 +262,60 @@ def _gelu_output_wants_fp16(rows: int) -> bool:
 
 
 def _linear_bias(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
-                 out_half: bool = False, math: Optional[int] = None) -> torch.Tensor:
-    """x @ weight^T + bias on the MFMA GEMM; `math` overrides the config's."""
+                 out_half: bool = False, math: Optional[int] = None,
+                 residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x @ weight^T + bias on the MFMA GEMM; `math` overrides the config's.
+
+    With `residual` (fp32, the output's shape) the result is residual + that,
+    the add done in the GEMM's epilogue where the kernel can (else added
+    here, and counted as a fallback).
+    """
     rows = x.numel() // x.shape[-1] if x.dim() >= 1 and x.shape[-1] else 0
     if (config.LINEAR_BIAS != "off" and bias is not None
             and rows <= config._LINEAR_BIAS_MAX_ROWS):
         kernels = _custom_kernels()
         if kernels is not None:
             code = config._GEMM_MATH_CODE[config.LINEAR_BIAS] if math is None else math
-            out = kernels.linear_bias(x, weight, bias, -1, code, out_half)
+            out = kernels.linear_bias(x, weight, bias, -1, code, out_half, residual=residual)
             if out is not None:
                 return out
+            if residual is not None:
+                out = kernels.linear_bias(x, weight, bias, -1, code, out_half)
+                if out is not None:
+                    fallback_counts["linear_bias_residual"] += 1
+                    return residual + out
     fallback_counts["linear_bias"] += 1
     out = F.linear(x.to(weight.dtype), weight, bias)
+    if residual is not None:
+        out = residual + out
     want = torch.float16 if out_half else torch.float32
     return out if out.dtype == want else out.to(want)
+
+
+def _residual_epilogue_wanted(width_in: int) -> bool:
+    """Fold the residual adds into out_proj's and ffn_out's epilogues?
+
+    Where the GEMM runs the pipelined kernel on fp16 operands (its K a
+    multiple of 64), the add+LayerNorm after it then becomes a plain
+    LayerNorm: one tensor read instead of two, none written back.
+    """
+    return (config.RESIDUAL_EPILOGUE != "off" and config.LINEAR_BIAS == "auto"
+            and width_in % 64 == 0 and width_in >= config._RESIDUAL_EPILOGUE_MIN_D)
+
+
+def _ffn_block_eligible(x, ffn_in, ffn_out) -> bool:
+    """Would _ffn_block run the fused kernel for this block (rather than decline)?"""
+    if config.FFN_BLOCK == "off":
+        return False
+    if (config.LINEAR_GELU != "auto" or config.LINEAR_BIAS != "auto"
+            or config.NORMED_FP16 == "off" or config.GELU_FP16 == "off"):
+        return False
+    if ffn_in.bias is None or ffn_out.bias is None or x.dtype != torch.float32:
+        return False
+    d_model, d_ff = x.shape[-1], ffn_in.weight.shape[0]
+    if config.FFN_BLOCK != "force" and d_model > config._FFN_BLOCK_MAX_D:
+        return False
+    return d_model <= 128 and d_ff <= 128 and d_model % 8 == 0 and d_ff % 8 == 0
 
 
 def _ffn_block(x, attn_out, norm1, ffn_in, ffn_out, norm2):

@@ -15,9 +15,10 @@ import torch.nn as nn
 from . import config
 from .kernels import (_add_layernorm, _add_layernorm_split, _add_layernorm_unpack,
                       _attention_dispatch, _attention_packed, _attention_wants_fp16,
-                      _ffn_block, _gelu_input_wants_fp16, _gelu_output_wants_fp16,
-                      _layernorm, _layernorm_split, _linear_bias, _linear_bias_split,
-                      _linear_gelu, _normed_split_wanted, _normed_wants_fp16, _qkv_math_code)
+                      _ffn_block, _ffn_block_eligible, _gelu_input_wants_fp16,
+                      _gelu_output_wants_fp16, _layernorm, _layernorm_split, _layernorm_unpack,
+                      _linear_bias, _linear_bias_split, _linear_gelu, _normed_split_wanted,
+                      _normed_wants_fp16, _qkv_math_code, _residual_epilogue_wanted)
 from .util import _version_or_none
 
 
@@ -95,17 +96,20 @@ class MySelfAttention(nn.Module):
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,
                 causal: bool = False, mask_is_trivial: bool = False,
-                packing=None) -> torch.Tensor:
+                packing=None, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         """`x` is [B, S, D], or [2, B, S, D] split fp16 planes of it (the form
-        a LayerNorm emits for the fp16x3 projection).
+        a LayerNorm emits for the split QKV projection).
 
         With `packing` (an optimized.packing.RowPacking), `x` holds only the
         valid rows, [T_valid, D] or planes [2, T_valid, D]; attention runs over
         the packed sequences and the result is [T_valid, D], with no padded
         rows to zero.
+
+        With `residual` (not on the masked padded path) the result is
+        residual + out_proj(...), the add done in out_proj's epilogue.
         """
         if packing is not None:
-            return self._forward_packed(x, causal, packing)
+            return self._forward_packed(x, causal, packing, residual)
         split = x.dim() == 4
         batch, seq_len = (x.shape[1], x.shape[2]) if split else (x.shape[0], x.shape[1])
         qkv_w, qkv_b = self._get_qkv_weight()
@@ -127,12 +131,18 @@ class MySelfAttention(nn.Module):
         attn_mask = valid_token_mask[:, None, None, :] if use_mask else None
         context = _attention_dispatch(q, k, v, attn_mask=attn_mask, is_causal=causal,
                                       scale=self.scale)
+        if residual is not None and not use_mask:
+            return _linear_bias(context, self.out_proj.weight, self.out_proj.bias,
+                                residual=residual)
         output = self.out_proj(context)
         if use_mask:
             output = output.masked_fill(~valid_token_mask[..., None], 0)
+        if residual is not None:
+            output = residual + output
         return output
 
-    def _forward_packed(self, x: torch.Tensor, causal: bool, packing) -> torch.Tensor:
+    def _forward_packed(self, x: torch.Tensor, causal: bool, packing,
+                        residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         split = x.dim() == 3
         rows = packing.t_valid
         qkv_w, qkv_b = self._get_qkv_weight()
@@ -145,6 +155,9 @@ class MySelfAttention(nn.Module):
         # [T_valid, 3, H, hd] -> three strided [T_valid, H, hd] views.
         q, k, v = qkv.view(rows, 3, self.num_heads, self.head_dim).unbind(1)
         context = _attention_packed(q, k, v, packing, causal, self.scale)
+        if residual is not None:
+            return _linear_bias(context, self.out_proj.weight, self.out_proj.bias,
+                                residual=residual)
         return self.out_proj(context)
 
 
@@ -178,8 +191,10 @@ class MyTransformerBlock(nn.Module):
         """
         if packing is not None:
             return self._forward_packed(x, normed, next_norm, next_norm_is_output, packing)
-        attn_out = self.attention(normed, valid_token_mask, self.causal, mask_is_trivial)
         use_mask = valid_token_mask is not None and not mask_is_trivial
+        if not use_mask and self._residual_fused(x):
+            return self._forward_residual_fused(x, normed, next_norm, next_norm_is_output)
+        attn_out = self.attention(normed, valid_token_mask, self.causal, mask_is_trivial)
 
         if not use_mask:
             fused = _ffn_block(x, attn_out, self.norm2, self.ffn_in, self.ffn_out, next_norm)
@@ -203,7 +218,40 @@ class MyTransformerBlock(nn.Module):
                          and _normed_wants_fp16(rows, x.shape[-1]))
         return _add_layernorm(x, ffn_out, next_norm, normed_half=trailing_half)
 
+    def _residual_fused(self, x: torch.Tensor) -> bool:
+        """Run out_proj and ffn_out with the residual adds in their epilogues?
+        Not where the fused FFN block will take the block's second half."""
+        d_model, d_ff = x.shape[-1], self.ffn_in.weight.shape[0]
+        rows = x.numel() // d_model
+        # the epilogue is the pipelined kernel's: fp16 operands in (ctx from
+        # attention, hidden from linear_gelu), K a multiple of 64
+        return (_residual_epilogue_wanted(d_model) and _residual_epilogue_wanted(d_ff)
+                and _attention_wants_fp16() and _gelu_output_wants_fp16(rows)
+                and not _ffn_block_eligible(x, self.ffn_in, self.ffn_out))
+
+    def _forward_residual_fused(self, x, normed, next_norm, next_norm_is_output, packing=None):
+        """The block with h1 = x + out_proj(...) and h2 = h1 + ffn_out(...)
+        formed in the GEMM epilogues (the same fp32 sums the add+LayerNorm
+        kernels would form), followed by plain LayerNorms of h1 and h2.
+        Outputs are bit-identical to the add+LayerNorm chain."""
+        rows = x.numel() // x.shape[-1]
+        width = x.shape[-1]
+        h1 = self.attention(normed, None, self.causal, True, packing=packing, residual=x)
+        normed2 = _layernorm(h1, self.norm2, out_half=_gelu_input_wants_fp16(rows, width))
+        hidden = _linear_gelu(normed2, self.ffn_in, out_half=_gelu_output_wants_fp16(rows))
+        h2 = _linear_bias(hidden, self.ffn_out.weight, self.ffn_out.bias, residual=h1)
+        if next_norm_is_output:
+            if packing is not None:
+                return None, _layernorm_unpack(h2, next_norm, packing)
+            return h2, _final_norm(h2, next_norm)
+        if _normed_split_wanted():
+            return h2, _layernorm_split(h2, next_norm)
+        return h2, _layernorm(h2, next_norm, out_half=_normed_wants_fp16(rows, width))
+
     def _forward_packed(self, x, normed, next_norm, next_norm_is_output, packing):
+        if self._residual_fused(x):
+            return self._forward_residual_fused(x, normed, next_norm, next_norm_is_output,
+                                                packing)
         attn_out = self.attention(normed, None, self.causal, True, packing=packing)
         if not next_norm_is_output:
             fused = _ffn_block(x, attn_out, self.norm2, self.ffn_in, self.ffn_out, next_norm)

@@ -152,6 +152,22 @@ int dotl_linear(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
                 int act, int math, int tile, void* stream);
 
 /*
+ * out[M, N] = residual[M, N] + act(x @ W^T + bias): dotl_linear with the
+ * residual add the following add+LayerNorm would do (reference
+ * csrc/add_layernorm.cuh:149-165, x_new = x + sub) moved into the GEMM's
+ * epilogue, the same fp32 sum. The layer uses it for out_proj (+ x) and
+ * ffn_out (+ h1); the LayerNorm after it then reads one tensor instead of
+ * two and writes none back. No counterpart entry in the reference, whose
+ * linear_bias (csrc/linear_gelu.cuh:598-719) the other arguments follow.
+ * fp32 out only; residual 16-byte aligned. Declines (DOTL_DECLINED) where
+ * the pipelined kernel does not run (fp32 x, K % 64 != 0): the caller adds
+ * the residual itself.
+ */
+int dotl_linear_residual(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
+                         const float* bias, const float* residual, float* out, int64_t M,
+                         int64_t N, int64_t K, int act, int math, int tile, void* stream);
+
+/*
  * Fused scaled-dot-product attention, flash style on MFMA.
  * Replaces fused_attention_forward
  * (reference csrc/attention_dispatch.cuh:332-519).

@@ -62,6 +62,9 @@ def test_linear_rejects_bad_codes(lib):
     assert lib.dotl_linear(None, 1, None, None, None, None, 0, 4, 4, 64, 0, 2, -1, None) == -1
     assert b"split fp16 planes" in lib.dotl_last_error()
     assert lib.dotl_linear(None, 2, None, None, None, None, 0, 0, 4, 64, 0, 2, -1, None) == 0
+    # the residual epilogue needs its residual
+    assert lib.dotl_linear_residual(None, 1, None, None, None, None, None, 4, 4, 64, 0, 0, -1,
+                                    None) == -1
     # tile ids beyond the menu
     assert lib.dotl_linear(None, 1, None, None, None, None, 0, 4, 4, 64, 0, 0, 14, None) == -1
     # empty problems launch nothing and succeed

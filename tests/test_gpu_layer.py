@@ -165,3 +165,25 @@ def test_native_library_is_loaded(kernels):
     """The product path runs libdotl_hip.so from the source tree, not a fallback."""
     maps = open("/proc/self/maps").read()
     assert kernel_ext.library_path() in maps
+
+
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C5"])
+def test_residual_epilogue_is_bit_identical(kernels, name):
+    """out_proj and ffn_out adding the residual stream in their epilogues (then
+    plain LayerNorms) give the add+LayerNorm chain's output bit for bit, on the
+    unpadded (C1) and packed-row (C2, C5) paths; no torch fallback runs."""
+    cfg = CONFIGS[name]
+    x, mask, params = make_case(cfg, batch=min(cfg.batch_size, 64))
+    saved = (ocfg.RESIDUAL_EPILOGUE, ocfg._RESIDUAL_EPILOGUE_MIN_D)
+    try:
+        outs = {}
+        ocfg._RESIDUAL_EPILOGUE_MIN_D = 0   # these widths sit below the speed threshold
+        for mode in ("auto", "off"):
+            ocfg.RESIDUAL_EPILOGUE = mode
+            okernels.fallback_counts.clear()
+            outs[mode], _ = _run_gpu(cfg, x, mask, params)
+            assert not okernels.fallback_counts, dict(okernels.fallback_counts)
+    finally:
+        ocfg.RESIDUAL_EPILOGUE, ocfg._RESIDUAL_EPILOGUE_MIN_D = saved
+    assert np.array_equal(outs["auto"], outs["off"])
+    assert compare_outputs(reference_layer(x, mask, params, cfg).numpy(), outs["auto"]).passed

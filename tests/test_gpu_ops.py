@@ -441,3 +441,20 @@ def test_gemm_dma_split_planes(kernels, M, N, K, tile, act):
                                  f"got {g[i]!r} want {want[i]!r} want16 {want16[i]!r} ulp {ulp[i]!r}")
     else:
         np.testing.assert_allclose(got.cpu().numpy(), want, atol=3e-6 * np.sqrt(K / 128), rtol=2e-6)
+
+
+@pytest.mark.parametrize("M,N,K", DMA_SHAPES)
+@pytest.mark.parametrize("tile", [-1, 3, 5, 9, 10, 12, 13])
+def test_gemm_residual_epilogue(kernels, M, N, K, tile):
+    """linear_bias(residual=R) = R + linear_bias() bit for bit: the epilogue adds
+    the same fp32 values in the same order as a separate add would."""
+    x, w, b = _gemm_case(M, N, K, 13 * M + N)
+    r = np.random.default_rng(M + K).standard_normal((M, N)).astype(np.float32)
+    xh, rt = _t(x).half(), _t(r)
+    plain = kernels.linear_bias(xh, _t(w), _t(b), tile, -1)
+    fused = kernels.linear_bias(xh, _t(w), _t(b), tile, -1, residual=rt)
+    assert torch.equal(fused, rt + plain)
+    # fp32 x takes the register-staged kernel, which declines the residual
+    assert kernels.linear_bias(_t(x), _t(w), _t(b), -1, -1, residual=rt) is None
+    with pytest.raises(RuntimeError, match="residual"):
+        kernels.linear_bias(xh, _t(w), _t(b), tile, -1, out_half=True, residual=rt)
