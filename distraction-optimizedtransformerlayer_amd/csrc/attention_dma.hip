@@ -72,7 +72,10 @@ __device__ __forceinline__ half4 lds_read_tr(const _Float16* p) {
     return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4_ptr)(p)));
 }
 
-template <int HD, int NW, int NS, bool OUT_F32>
+// MASK: an explicit mask may be present. Its per-element loads hold many
+// registers, so unmasked calls (the sequence tail and causal limits are
+// compares only) take the variant without that code.
+template <int HD, int NW, int NS, bool OUT_F32, bool MASK>
 __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(AttnParams p) {
     using TL = AttnTile<HD>;
     constexpr int KS = HD / 16;            // k-steps of the score product
@@ -144,7 +147,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
     // below count DMAs only.
     wait_vmcnt<0>();
 
-    const bool has_mask = p.mask != nullptr;
+    const bool has_mask = MASK && p.mask != nullptr;
     const bool key_only_mask = has_mask && p.mq == 0;
     const uint8_t* mbase = has_mask ? p.mask + b * p.mb + h * p.mh : nullptr;
 
@@ -181,25 +184,25 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
         const int lc = (lane % TL::CPR) ^ (is_v ? TL::fv(r) : TL::fk(r));
         lane_off[j] = static_cast<unsigned>((static_cast<int64_t>(r) * p.ss + lc * 8) * 2);
     }
-    auto issue = [&](int kt, _Float16* ks_, _Float16* vs_) __attribute__((always_inline)) {
+    auto issue_one = [&](auto jj, int kt, _Float16* ks_, _Float16* vs_) __attribute__((always_inline)) {
+        constexpr int j = decltype(jj)::value;
         const int key0 = kt * kKB;
-        const bool full_tile = key0 + kKB <= S;
-#pragma unroll
-        for (int j = 0; j < L; ++j) {
-            const int i = wave + NW * j;
-            const bool is_v = i >= TL::NDMA;
-            const int ii = is_v ? i - TL::NDMA : i;
-            _Float16* dst = (is_v ? vs_ : ks_) + ii * TL::RPD * HD;
-            if (full_tile) {
-                const _Float16* base = (is_v ? vbase : kbase) + static_cast<int64_t>(key0) * p.ss;
-                dma16_off(base, lane_off[j], dst);
-            } else {
-                const int r = ii * TL::RPD + lane / TL::CPR;
-                const int lc = (lane % TL::CPR) ^ (is_v ? TL::fv(r) : TL::fk(r));
-                const int key = min(key0 + r, S - 1);
-                dma16((is_v ? vbase : kbase) + static_cast<int64_t>(key) * p.ss + lc * 8, dst);
-            }
+        const int i = wave + NW * j;
+        const bool is_v = i >= TL::NDMA;
+        const int ii = is_v ? i - TL::NDMA : i;
+        _Float16* dst = (is_v ? vs_ : ks_) + ii * TL::RPD * HD;
+        if (key0 + kKB <= S) {
+            const _Float16* base = (is_v ? vbase : kbase) + static_cast<int64_t>(key0) * p.ss;
+            dma16_off(base, lane_off[j], dst);
+        } else {
+            const int r = ii * TL::RPD + lane / TL::CPR;
+            const int lc = (lane % TL::CPR) ^ (is_v ? TL::fv(r) : TL::fk(r));
+            const int key = min(key0 + r, S - 1);
+            dma16((is_v ? vbase : kbase) + static_cast<int64_t>(key) * p.ss + lc * 8, dst);
         }
+    };
+    auto issue = [&](int kt, _Float16* ks_, _Float16* vs_) __attribute__((always_inline)) {
+        static_for<0, L>([&](auto jj) { issue_one(jj, kt, ks_, vs_); });
     };
 
     floatx16 o[HT];
@@ -208,23 +211,87 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
     float m_run = -INFINITY;
     float l_run = 0.f;
 
-    auto compute = [&](int kt, const _Float16* ks_, const _Float16* vs_) __attribute__((always_inline)) {
-        const int key0 = kt * kKB;
-        if (p.causal && key0 > q_w0 + 31) return;   // every query of this wave precedes the tile
+    // V^T fragment (key step t, hd tile j) for O^T += V^T P^T: MFMA step t
+    // covers keys 32 (t/2) + 16 (t%2) + {8 (e/4) + 4 lg + e%4}, two transposed
+    // reads of 4 keys each (rows kb .. kb+3 and kb+8 .. kb+11).
+    //
+    // Fragment addresses. K fragment (k-step ks, keys 32 t2 + lr) is chunk
+    // (2 ks + lg) ^ fk(row) of its row; V^T fragment (t, j) reads rows
+    // 16 t + 4 lg + trow (+ 8), chunk (4 j + tchunk) ^ fv(row). fk and fv are
+    // periodic in the row with a period dividing 8, and the chunk index terms
+    // 2 ks and 4 j occupy bits the lane's own terms leave clear, so every
+    // fragment's byte offset within a stage is the lane's first one XOR
+    // 32 ks (K) or 64 j (V), plus a constant for t2, t and the second row
+    // group. Only the two base offsets stay live across the loop.
+    const int trow = (lane & 15) >> 2;
+    const int tchunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    const int thalf = 4 * (lane & 1);
+    const unsigned k_off0 = static_cast<unsigned>((lr * HD + ((lg ^ TL::fk(lr)) * 8)) * 2);
+    const unsigned v_off0 = static_cast<unsigned>(
+        ((4 * lg + trow) * HD + ((tchunk ^ TL::fv(4 * lg + trow)) * 8) + thalf) * 2);
+    auto vread = [&](const _Float16* vs_, unsigned vofs, int t, int j) __attribute__((always_inline))
+        -> half8 {
+        const char* a = reinterpret_cast<const char*>(vs_) + (vofs ^ (64u * j)) + t * (32 * HD);
+        const half4 a4 = lds_read_tr(reinterpret_cast<const _Float16*>(a));
+        const half4 b4 = lds_read_tr(reinterpret_cast<const _Float16*>(a + 16 * HD));
+        return __builtin_shufflevector(a4, b4, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    auto kread = [&](const _Float16* ks_, unsigned kofs, int ks, int t2) __attribute__((always_inline))
+        -> half8 {
+        const char* a = reinterpret_cast<const char*>(ks_) + (kofs ^ (32u * ks)) + t2 * (64 * HD);
+        return *reinterpret_cast<const half8*>(a);
+    };
 
+    // One key tile. LDS fragments are read KD k-steps (K) and VD MFMAs (V)
+    // ahead of their MFMAs, with scheduling fences holding that order: left
+    // to itself the compiler reads each fragment into one register set right
+    // before its MFMA, exposing the full LDS latency on every MFMA. `dma(j)`
+    // issues this wave's j-th DMA of the tile being refilled; the L of them
+    // are spread over the score k-steps instead of leaving every wave of the
+    // workgroup queued on the address unit at once after the barrier.
+    auto compute = [&](int kt, const _Float16* ks_, const _Float16* vs_, auto&& dma)
+                       __attribute__((always_inline)) {
+        const int key0 = kt * kKB;
+        if (p.causal && key0 > q_w0 + 31) {   // every query of this wave precedes the tile
+            static_for<0, L>(dma);
+            return;
+        }
+
+        // Opaque per tile, so the compiler derives the addresses here instead
+        // of hoisting one register per fragment and stage out of the loop.
+        unsigned kofs = k_off0, vofs = v_off0;
+        asm volatile("" : "+v"(kofs), "+v"(vofs));
+
+        constexpr int KD = KS < 2 ? KS : 2;
+        half8 kf[KS][2];
+        static_for<0, KD>([&](auto kk) {
+            kf[kk][0] = kread(ks_, kofs, kk, 0);
+            kf[kk][1] = kread(ks_, kofs, kk, 1);
+        });
         floatx16 s[2];
         s[0] = floatx16{};
         s[1] = floatx16{};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-            for (int t2 = 0; t2 < 2; ++t2) {
-                const int row = t2 * 32 + lr;
-                const int pc = (ks * 2 + lg) ^ TL::fk(row);
-                const half8 kf = *reinterpret_cast<const half8*>(ks_ + row * HD + pc * 8);
-                s[t2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[t2], 0, 0, 0);
+        static_for<0, KS>([&](auto kk) {
+            constexpr int ks = decltype(kk)::value;
+            if constexpr (ks + KD < KS) {
+                kf[ks + KD][0] = kread(ks_, kofs, ks + KD, 0);
+                kf[ks + KD][1] = kread(ks_, kofs, ks + KD, 1);
             }
-        }
+            static_for<0, L>([&](auto jj) {
+                if constexpr (decltype(jj)::value * KS / L == ks) dma(jj);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            s[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks][0], qf[ks], s[0], 0, 0, 0);
+            s[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks][1], qf[ks], s[1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+
+        // The first V fragments load while the softmax runs.
+        constexpr int NV = 4 * HT;
+        constexpr int VD = NV < 4 ? NV : 4;
+        half8 vf[NV];
+        static_for<0, VD>([&](auto ii) { vf[ii] = vread(vs_, vofs, ii / HT, ii % HT); });
+        __builtin_amdgcn_sched_barrier(0);
 
         // Softmax in the log2 domain with c = scale * log2(e): the maximum is
         // taken over the raw scores and scaled once, and each probability is
@@ -246,14 +313,19 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
                 const int key = key0 + lane;
                 live = __ballot(key < S && mbase[static_cast<int64_t>(key) * p.mk] != 0);
             }
+            // Key key0 + 4 lg + c is in range (and not after this lane's
+            // query) iff c <= lim: one compare against a literal per score.
+            int lim = S - 1 - key0;
+            if (p.causal) lim = min(lim, my_q - key0);
+            lim -= 4 * lg;
 #pragma unroll
             for (int t2 = 0; t2 < 2; ++t2) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int kl = t2 * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+                    const int cl = t2 * 32 + 8 * (r >> 2) + (r & 3);
+                    const int kl = cl + 4 * lg;
                     const int key = key0 + kl;
-                    bool ok = key < S;
-                    if (p.causal) ok = ok && key <= my_q;
+                    bool ok = cl <= lim;
                     if (has_mask) {
                         if (key_only_mask) {
                             ok = ok && ((live >> kl) & 1ull);
@@ -303,28 +375,17 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
                 for (int r = 0; r < 16; ++r) o[j][r] *= corr;
         }
 
-        // O^T[hd, q] += V^T[hd, keys] P^T[keys, q]. MFMA step t covers keys
-        // 32 (t/2) + 16 (t%2) + {8 (e/4) + 4 lg + e%4}: two transposed reads
-        // of 4 keys each (rows kb .. kb+3 and kb+8 .. kb+11).
-        const int hsel = (lane >> 4) & 1;
-        const int trow = (lane & 15) >> 2;
-        const int tchunk = 2 * hsel + ((lane & 3) >> 1);
-        const int thalf = 4 * (lane & 1);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int kb = 32 * (t >> 1) + 16 * (t & 1) + 4 * lg;
-            const int ra = kb + trow;
-            const int rb = ra + 8;
-#pragma unroll
-            for (int j = 0; j < HT; ++j) {
-                const int c = 4 * j + tchunk;
-                const half4 a4 = lds_read_tr(vs_ + ra * HD + ((c ^ TL::fv(ra)) * 8) + thalf);
-                const half4 b4 = lds_read_tr(vs_ + rb * HD + ((c ^ TL::fv(rb)) * 8) + thalf);
-                const half8 vf = __builtin_shufflevector(a4, b4, 0, 1, 2, 3, 4, 5, 6, 7);
-                o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], o[j], 0, 0, 0);
-            }
-        }
+        // O^T[hd, q] += V^T[hd, keys] P^T[keys, q], key step t outer.
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<0, NV>([&](auto ii) {
+            constexpr int i = decltype(ii)::value;
+            if constexpr (i + VD < NV) vf[i + VD] = vread(vs_, vofs, (i + VD) / HT, (i + VD) % HT);
+            __builtin_amdgcn_sched_barrier(0);
+            o[i % HT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[i], pf[i / HT], o[i % HT], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        });
     };
+    auto no_dma = [](auto) __attribute__((always_inline)) {};
 
     // Wait for tile kt's DMAs: younger tiles already issued are
     // min(NS - 2, nkt - 1 - kt), each L instructions.
@@ -348,7 +409,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
             issue(kt, k0s, v0s);
             wait_vmcnt<0>();
             stage_barrier();
-            compute(kt, k0s, v0s);
+            compute(kt, k0s, v0s, no_dma);
         }
     } else {
     auto prologue = [&](auto s) __attribute__((always_inline)) {
@@ -367,10 +428,13 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
             constexpr int NEXT = (I + NS - 1) % NS;
             wait_tile(kt);
             stage_barrier();
-            if (kt + NS - 1 < nkt)
-                issue(kt + NS - 1, kst(std::integral_constant<int, NEXT>{}),
-                      vst(std::integral_constant<int, NEXT>{}));
-            compute(kt, kst(s), vst(s));
+            const bool refill = kt + NS - 1 < nkt;
+            auto dma = [&](auto jj) __attribute__((always_inline)) {
+                if (refill)
+                    issue_one(jj, kt + NS - 1, kst(std::integral_constant<int, NEXT>{}),
+                              vst(std::integral_constant<int, NEXT>{}));
+            };
+            compute(kt, kst(s), vst(s), dma);
         }
     };
     int kt = 0;
@@ -580,9 +644,19 @@ void launch_short(const AttnParams& p, hipStream_t stream) {
 
 template <int HD, int NW, int NS, bool OUT_F32>
 void launch_one(const AttnParams& p, hipStream_t stream) {
+    if (p.mask != nullptr) {
+        // Masked calls run one configuration (4 waves, 2 stages) whatever
+        // the pipeline choice: the result does not depend on it.
+        AttnParams pm = p;
+        pm.nqb = (p.S + 127) / 128;
+        const int64_t blocks = static_cast<int64_t>(pm.nqb) * p.B * p.H;
+        hipLaunchKernelGGL((attn_dma_kernel<HD, 4, 2, OUT_F32, true>),
+                           dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, pm);
+        return;
+    }
     const int64_t blocks = static_cast<int64_t>(p.nqb) * p.B * p.H;
-    hipLaunchKernelGGL((attn_dma_kernel<HD, NW, NS, OUT_F32>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(NW * 64), 0, stream, p);
+    hipLaunchKernelGGL((attn_dma_kernel<HD, NW, NS, OUT_F32, false>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0, stream, p);
 }
 
 // Deepest pipeline whose in-flight DMA count fits vmcnt (6 bits).

@@ -86,15 +86,6 @@ struct DmaLayout {
     __device__ __forceinline__ static int swz(int row) { return (row / SWZ_DIV) % CPR; }
 };
 
-// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
-template <int B, int E, typename Fn>
-__device__ __forceinline__ void static_for(Fn&& f) {
-    if constexpr (B < E) {
-        f(std::integral_constant<int, B>{});
-        static_for<B + 1, E>(f);
-    }
-}
-
 template <int BM, int BN, int BK, int NS, int MODE, int ACT, bool OUT_F16>
 struct DmaGemm {
     using L = DmaLayout<BM, BN, BK, MODE>;
