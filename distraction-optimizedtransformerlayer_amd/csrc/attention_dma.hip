@@ -249,12 +249,19 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
     // issues this wave's j-th DMA of the tile being refilled; the L of them
     // are spread over the score k-steps instead of leaving every wave of the
     // workgroup queued on the address unit at once after the barrier.
-    auto compute = [&](int kt, const _Float16* ks_, const _Float16* vs_, auto&& dma)
+    // `check` (a bool constant): whether the tile can lie wholly after this
+    // wave's queries under the causal limit, in which case it is skipped.
+    // Tiles that no wave skips run without the test, whose merge of skipped
+    // and updated accumulators would otherwise cost a register copy of O^T
+    // every tile.
+    auto compute = [&](int kt, const _Float16* ks_, const _Float16* vs_, auto&& dma, auto check)
                        __attribute__((always_inline)) {
         const int key0 = kt * kKB;
-        if (p.causal && key0 > q_w0 + 31) {   // every query of this wave precedes the tile
-            static_for<0, L>(dma);
-            return;
+        if constexpr (decltype(check)::value) {
+            if (p.causal && key0 > q_w0 + 31) {   // every query of this wave precedes the tile
+                static_for<0, L>(dma);
+                return;
+            }
         }
 
         // Opaque per tile, so the compiler derives the addresses here instead
@@ -343,7 +350,13 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
         for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
             for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[t2][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave)) * c;
+        {
+            // Lanes l and l ^ 32 hold the two halves of one query's keys:
+            // v_permlane32_swap exchanges the wave's halves in registers.
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax),
+                                                             __float_as_uint(tmax), false, false);
+            tmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
+        }
         float corr = 1.f;
         if (tmax > m_run + kLazyTau) {
             corr = __builtin_amdgcn_exp2f(m_run - tmax);   // 0 while m_run is -inf
@@ -409,7 +422,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
             issue(kt, k0s, v0s);
             wait_vmcnt<0>();
             stage_barrier();
-            compute(kt, k0s, v0s, no_dma);
+            compute(kt, k0s, v0s, no_dma, std::true_type{});
         }
     } else {
     auto prologue = [&](auto s) __attribute__((always_inline)) {
@@ -422,7 +435,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
     prologue(std::integral_constant<int, 1>{});
     prologue(std::integral_constant<int, 2>{});
 
-    auto step = [&](auto s, int kt) __attribute__((always_inline)) {
+    auto step = [&](auto s, int kt, auto check) __attribute__((always_inline)) {
         constexpr int I = decltype(s)::value;
         if constexpr (I < NS) {
             constexpr int NEXT = (I + NS - 1) % NS;
@@ -434,19 +447,30 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
                     issue_one(jj, kt + NS - 1, kst(std::integral_constant<int, NEXT>{}),
                               vst(std::integral_constant<int, NEXT>{}));
             };
-            compute(kt, kst(s), vst(s), dma);
+            compute(kt, kst(s), vst(s), dma, check);
         }
     };
+    // Tiles every wave computes: all of them, or under the causal limit
+    // those up to the first query of the workgroup.
+    const int nfree = p.causal ? min(nkt, (q_wg0 + 31) / kKB + 1) : nkt;
+    const std::false_type all_waves;
+    const std::true_type some_waves;
     int kt = 0;
-    for (; kt + NS <= nkt; kt += NS) {
-        step(std::integral_constant<int, 0>{}, kt);
-        step(std::integral_constant<int, 1>{}, kt + 1);
-        step(std::integral_constant<int, 2>{}, kt + 2);
-        step(std::integral_constant<int, 3>{}, kt + 3);
+    for (; kt + NS <= nfree; kt += NS) {
+        step(std::integral_constant<int, 0>{}, kt, all_waves);
+        step(std::integral_constant<int, 1>{}, kt + 1, all_waves);
+        step(std::integral_constant<int, 2>{}, kt + 2, all_waves);
+        step(std::integral_constant<int, 3>{}, kt + 3, all_waves);
     }
-    if (kt < nkt) step(std::integral_constant<int, 0>{}, kt);
-    if (kt + 1 < nkt) step(std::integral_constant<int, 1>{}, kt + 1);
-    if (kt + 2 < nkt) step(std::integral_constant<int, 2>{}, kt + 2);
+    for (; kt + NS <= nkt; kt += NS) {
+        step(std::integral_constant<int, 0>{}, kt, some_waves);
+        step(std::integral_constant<int, 1>{}, kt + 1, some_waves);
+        step(std::integral_constant<int, 2>{}, kt + 2, some_waves);
+        step(std::integral_constant<int, 3>{}, kt + 3, some_waves);
+    }
+    if (kt < nkt) step(std::integral_constant<int, 0>{}, kt, some_waves);
+    if (kt + 1 < nkt) step(std::integral_constant<int, 1>{}, kt + 1, some_waves);
+    if (kt + 2 < nkt) step(std::integral_constant<int, 2>{}, kt + 2, some_waves);
     }
 
     // Normalise and store: O^T register r of tile j at lane l is hd row

@@ -82,6 +82,28 @@ def test_layernorm_parity(kernels, rows, D, with_sub):
     assert np.all(np.abs(nh.cpu().float().numpy() - want16) <= ulp + 1e-7)
 
 
+@pytest.mark.parametrize("D", [256, 512])
+def test_layernorm_tall_gather_with_dropped_rows(kernels, D):
+    """The packed-row gather over a tall input (70K rows from 90K): rows whose
+    index is out of range come out zero, the rest equal the dense LayerNorm
+    of the indexed row."""
+    in_rows = 90000
+    g = torch.Generator().manual_seed(D)
+    x = torch.randn(in_rows, D, generator=g).to(DEV)
+    w = torch.randn(D, generator=g).to(DEV)
+    b = torch.randn(D, generator=g).to(DEV)
+    idx = torch.randint(0, in_rows, (70003,), generator=g, dtype=torch.int32)
+    idx[::11] = -1
+    idx[5::13] = in_rows + 7
+    idx = idx.to(DEV)
+    rows, normed = kernels.fused_layernorm_rows(x, w, b, idx, 1e-5, "float", True)
+    dense = kernels.fused_layernorm(x, w, b, 1e-5, False)
+    ok = (idx >= 0) & (idx < in_rows)
+    assert torch.equal(rows[ok], x.index_select(0, idx[ok].long()))
+    assert torch.equal(normed[ok], dense.index_select(0, idx[ok].long()))
+    assert torch.count_nonzero(rows[~ok]) == 0 and torch.count_nonzero(normed[~ok]) == 0
+
+
 @pytest.mark.parametrize("mean,scale", [(1e4, 1.0), (1e5, 1e-2)])
 def test_layernorm_large_mean_rows(kernels, mean, scale):
     """Large-mean rows against the fp64 definition (reference verify_layernorm_warp.py:37-45)."""
