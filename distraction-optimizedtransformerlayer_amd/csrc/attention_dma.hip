@@ -369,8 +369,8 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
         const half2v one2 = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
         float lsum = 0.f;
         half8 pf[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        auto make_p = [&](auto tt) __attribute__((always_inline)) {
+            constexpr int t = decltype(tt)::value;
 #pragma unroll
             for (int e = 0; e < 8; ++e)
                 pf[t][e] = to_half(__builtin_amdgcn_exp2f(fmaf(s[t >> 1][8 * (t & 1) + e], c, neg_m)));
@@ -379,8 +379,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
                 const half2v pr = {pf[t][e], pf[t][e + 1]};
                 lsum = __builtin_amdgcn_fdot2(pr, one2, lsum, false);
             }
-        }
-        l_run = l_run * corr + lsum;
+        };
         if (__any(corr != 1.f)) {
 #pragma unroll
             for (int j = 0; j < HT; ++j)
@@ -388,15 +387,32 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
                 for (int r = 0; r < 16; ++r) o[j][r] *= corr;
         }
 
-        // O^T[hd, q] += V^T[hd, keys] P^T[keys, q], key step t outer.
+        // O^T[hd, q] += V^T[hd, keys] P^T[keys, q], key step t outer. P of
+        // step t + 1 is formed while the MFMAs of step t run: they do not
+        // depend on it, so the wave issues that VALU work in their shadow.
+        // The group barriers lay each step out as: per MFMA, the V reads it
+        // prefetches, the MFMA, then a share of the next step's P.
+        make_p(std::integral_constant<int, 0>{});
         __builtin_amdgcn_sched_barrier(0);
-        static_for<0, NV>([&](auto ii) {
-            constexpr int i = decltype(ii)::value;
-            if constexpr (i + VD < NV) vf[i + VD] = vread(vs_, vofs, (i + VD) / HT, (i + VD) % HT);
-            __builtin_amdgcn_sched_barrier(0);
-            o[i % HT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[i], pf[i / HT], o[i % HT], 0, 0, 0);
+        constexpr int kValuPerMfma = (24 + HT - 1) / HT;
+        static_for<0, 4>([&](auto tt) {
+            constexpr int t = decltype(tt)::value;
+            static_for<0, HT>([&](auto jj) {
+                constexpr int j = decltype(jj)::value;
+                constexpr int i = t * HT + j;
+                if constexpr (i + VD < NV) vf[i + VD] = vread(vs_, vofs, (i + VD) / HT, (i + VD) % HT);
+                o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[i], pf[t], o[j], 0, 0, 0);
+            });
+            if constexpr (t + 1 < 4) make_p(std::integral_constant<int, t + 1>{});
+            static_for<0, HT>([&](auto jj) {
+                constexpr int i = t * HT + decltype(jj)::value;
+                if constexpr (i + VD < NV) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if constexpr (t + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);
+            });
             __builtin_amdgcn_sched_barrier(0);
         });
+        l_run = l_run * corr + lsum;
     };
     auto no_dma = [](auto) __attribute__((always_inline)) {};
 
