@@ -345,11 +345,20 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
                 }
             }
         }
-        float tmax = -INFINITY;
+        // Row maximum over NCH independent chains (max is exact, so the order
+        // does not matter). Four chains cut the dependent depth; measured on
+        // MI355X that gains 2-3% at head_dim 128 and loses 1-3% at 64.
+        constexpr int NCH = HD >= 128 ? 4 : 1;
+        float mx[NCH];
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) mx[k] = -INFINITY;
 #pragma unroll
         for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[t2][r]);
+            for (int r = 0; r < 16; ++r) mx[r % NCH] = fmaxf(mx[r % NCH], s[t2][r]);
+        float tmax = mx[0];
+#pragma unroll
+        for (int k = 1; k < NCH; ++k) tmax = fmaxf(tmax, mx[k]);
         {
             // Lanes l and l ^ 32 hold the two halves of one query's keys:
             // v_permlane32_swap exchanges the wave's halves in registers.
