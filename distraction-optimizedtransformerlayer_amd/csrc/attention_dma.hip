@@ -572,13 +572,18 @@ __global__ __launch_bounds__(256) void attn_short_kernel(AttnParams p) {
     const _Float16* vbase = static_cast<const _Float16*>(p.v) + seq_off + h * p.sh;
     _Float16* vs = vsh + wave * SZ;
 
-    // V rows 0..31 (keys past the sequence clamped to its last row).
+    // V rows 0..15, and 16..31 when the sequence reaches them (keys past the
+    // sequence clamped to its last row). Without them the second PV step
+    // is skipped: its P is 0 there, and unloaded rows could hold NaNs.
+    const bool two_steps = S > 16;
 #pragma unroll
     for (int j = 0; j < ND; ++j) {
-        const int r = j * TL::RPD + lane / TL::CPR;
-        const int lc = (lane % TL::CPR) ^ TL::fv(r);
-        const int key = min(r, S - 1);
-        dma16(vbase + static_cast<int64_t>(key) * p.ss + lc * 8, vs + j * TL::RPD * HD);
+        if (j < ND / 2 || two_steps) {
+            const int r = j * TL::RPD + lane / TL::CPR;
+            const int lc = (lane % TL::CPR) ^ TL::fv(r);
+            const int key = min(r, S - 1);
+            dma16(vbase + static_cast<int64_t>(key) * p.ss + lc * 8, vs + j * TL::RPD * HD);
+        }
     }
 
     const int my_q = lr;
@@ -644,6 +649,7 @@ __global__ __launch_bounds__(256) void attn_short_kernel(AttnParams p) {
     const int thalf = 4 * (lane & 1);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
+        if (t == 1 && !two_steps) break;
         const int ra = 16 * t + 4 * lg + trow;
         const int rb = ra + 8;
 #pragma unroll

@@ -210,7 +210,7 @@ def test_packed_graph_reloads_maps_for_a_new_mask(kernels):
         ocfg.ROW_PACKING, ocfg.CUDA_GRAPH = prev
 
 
-@pytest.mark.parametrize("S", [1, 5, 16, 32])
+@pytest.mark.parametrize("S", [1, 5, 16, 17, 32])
 @pytest.mark.parametrize("hd", [32, 64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 def test_short_sequence_kernel_equals_tiled(kernels, S, hd, causal):
