@@ -485,6 +485,13 @@ bool dispatch_tile(const DmaArgs& a, int tile) {
             if constexpr (PASSES == 1) launch_dma<128, 64, 64, 3, MODE, ACT, OUT_F16>(a);
             else launch_dma<128, 64, 64, 2, MODE, ACT, OUT_F16>(a);
             return true;
+        // 192x128: fewer, larger tiles where 128-row tiles leave a short
+        // second wave of workgroups. 320 / 512 rows: 40 / 64 KiB a stage
+        // (three passes would not fit two stages).
+        case 14:
+            if constexpr (PASSES == 1) { launch_dma<192, 128, 64, 3, MODE, ACT, OUT_F16>(a); return true; }
+            else if constexpr (PASSES == 2) { launch_dma<192, 128, 64, 2, MODE, ACT, OUT_F16>(a); return true; }
+            return false;
     }
     return false;
 }
@@ -497,8 +504,11 @@ bool dispatch_tile(const DmaArgs& a, int tile) {
 //     workgroup per CU; else the 128x128 two-stage tile (two workgroups a
 //     CU) when it fills the CUs four times over, or at short K; else
 //     128x64, then 64x64;
-//   * split passes: the 128x128 tile with 128-byte K rows when it fills the
-//     CUs, else the shallow 128x64, then 64x64.
+//   * split passes: two passes at K <= 512 on the 192x128 tile (C2's QKV,
+//     M = 3487: 228 tiles in one wave instead of a short second wave of
+//     128-row tiles, 20.5 vs 23.8 us; C5's: 125.8 vs 130.9 us; at K = 1024
+//     and 2048 it loses); else the 128x128 tile with 128-byte K rows when it
+//     fills the CUs, else the shallow 128x64, then 64x64.
 int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     if (passes == 1) {
@@ -508,6 +518,7 @@ int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
         if (tiles(128, 64) >= 200) return 13;
         return 8;
     }
+    if (passes == 2 && K <= 512 && tiles(192, 128) >= 200) return 14;
     if (tiles(128, 128) >= 400) return 10;
     if (tiles(128, 64) >= 240) return 7;
     return 8;
