@@ -1,0 +1,4 @@
+// The pipelined and short-sequence attention kernels for head_dim 64.
+#include "attention_dma_impl.h"
+
+DOTL_ATTN_DMA_INSTANTIATE(64)

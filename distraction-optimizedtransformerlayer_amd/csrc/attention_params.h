@@ -37,6 +37,12 @@ inline int attn_query_blocks(int S) {
 bool launch_attn_dma(const AttnParams& p, int head_dim, bool out_f32, int nw, int ns,
                      hipStream_t stream);
 
+namespace attn_dma {
+// launch_attn_dma for one head_dim (32, 64 or 128), in attention_dma_hd*.hip.
+template <int HD>
+bool launch_head_dim(const AttnParams& p, bool out_f32, int nw, int ns, hipStream_t stream);
+}  // namespace attn_dma
+
 // The exact fp32 kernel (attention_scalar.hip): q/k/v fp16 or fp32, any
 // head_dim in [1, kMaxScalarHeadDim], `scale` applied to the raw dot
 // products. Sizes its own grid (p.nqb is ignored); false when head_dim is

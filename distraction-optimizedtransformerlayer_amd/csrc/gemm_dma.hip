@@ -1,502 +1,11 @@
-// out = act(x @ W^T + bias) on gfx950 MFMA, operands streamed HBM -> LDS by
-// the LDS-DMA loads (global_load_lds_dwordx4), NS pipeline stages deep.
-//
-// The fast path behind dotl_linear for fp16 operands (x fp16, or x as split
-// fp16 hi/lo planes) with K a multiple of 64; gemm.hip's register-staged
-// kernel serves everything else (fp32 x, ragged K).
-//
-// MI355X design:
-//   * no staging registers: each lane's 16-byte load lands directly in LDS
-//     (the wave's 64 lanes fill one contiguous 1 KiB run, lane l at +16 l),
-//     so the pipeline can be 4-8 stages deep (up to 144 KiB of the CU's
-//     160 KiB LDS) without spending VGPRs. Measured on MI355X, a CU's
-//     operand stream is latency-bound: ~1.6 us per 64 KiB batch in flight,
-//     so feeding a 256x256 tile at the MFMA rate takes ~100 KiB in flight.
-//     K tiles are therefore 32 deep (BK = 32: 32 KiB per 256x256 stage) and
-//     the stages many, NS - 1 of them in flight while one is multiplied;
-//   * each stage is its own __shared__ array and the K loop is unrolled by
-//     NS, so every LDS read names a stage the in-flight DMA provably does not
-//     write: the compiler then adds no conservative vmcnt(0) before the reads;
-//     the kernel waits itself, for exactly the loads of the tile it is about
-//     to read (vmcnt = loads of the younger tiles still allowed in flight);
-//   * LDS rows are BK*2 bytes with the 16-byte chunks XOR-swizzled: a
-//     ds_read_b128 serves 16 lanes per pass over the 64 four-byte banks, and
-//     the 16 rows a fragment read touches then sit on 16 distinct 16-byte
-//     bank groups (chunk ^ (row / rows-per-256B) % chunks-per-row),
-//     conflict-free without padding (which would break the DMA's contiguous
-//     lane layout; measured with SQ_LDS_BANK_CONFLICT on an LDS-only loop:
-//     zero, against 2-way for a 128-byte sweep and 4-way unswizzled). The
-//     swizzle is applied on the global side: each DMA lane writes a fixed
-//     physical chunk and loads the logical chunk that maps there;
-//   * rows past M (or N) are clamped to the last valid row -- those outputs
-//     are never stored -- so every DMA is in bounds and branch-free; K must
-//     be a multiple of 64 (no K tail);
-//   * MODE (bit 0: split W, bit 1: split x) sets the passes: 0 x*W; 1
-//     x*W + 2^-12 x*lo(W) (x exact in fp16); 2 hi(x)*W + 2^-12 lo(x)*W (x
-//     given as fp16 hi/lo planes, W in fp16); 3 all three products: the
-//     lo terms in a second fp32 accumulator;
-//   * 2 x 2 wavefronts, each a (BM/2) x (BN/2) block of 32x32 accumulators,
-//     issued as W x A^T so every accumulator holds a C^T tile: each lane then
-//     owns runs of 4 consecutive output columns of one row, and the epilogue
-//     (bias from LDS, GELU, narrowing) stores them 16 or 8 bytes at a time
-//     from one row address per tile. The epilogue's cost matters here: with
-//     one workgroup per CU nothing overlaps it, and at the configs' short K
-//     (256-512) it was costing more than the MFMAs.
-#include "dotl_dma.h"
+// The pipelined GEMM's tile choice and entry point. The kernels are in
+// gemm_dma_impl.h, instantiated per arithmetic mode in gemm_dma_mode*.hip.
+#include "gemm_dma.h"
 
 namespace dotl {
 
-namespace {
-
-constexpr int kThreads = 256;
-constexpr int kXcds = 8;
-constexpr int kGroupM = 8;
-
-__device__ __forceinline__ void tile_of(int64_t id, int64_t nm, int64_t nn, int64_t& mt,
-                                        int64_t& nt) {
-    const int64_t total = nm * nn;
-    const int64_t per = total / kXcds;
-    if (id < per * kXcds) id = (id % kXcds) * per + id / kXcds;
-    const int64_t in_group = kGroupM * nn;
-    const int64_t group = id / in_group;
-    const int64_t first_m = group * kGroupM;
-    const int64_t gsize = min(static_cast<int64_t>(kGroupM), nm - first_m);
-    const int64_t r = id - group * in_group;
-    mt = first_m + r % gsize;
-    nt = r / gsize;
-}
-
-template <int BM, int BN, int BK, int MODE>
-struct DmaLayout {
-    // rows of BK halves in one stage: A, W, then lo(W) (MODE & 1), lo(A) (MODE & 2)
-    static constexpr bool SW = (MODE & 1) != 0;
-    static constexpr bool SA = (MODE & 2) != 0;
-    static constexpr int CPR = BK / 8;               // 16-byte chunks per row
-    static constexpr int ROWS_PER_DMA = 64 / CPR;    // rows one wave instruction fills
-    static constexpr int ROWS_PER_ROUND = 4 * ROWS_PER_DMA;
-    static constexpr int SWZ_DIV = 256 / (BK * 2);   // rows per 256-byte bank sweep
-    static constexpr int A_ROW = 0;
-    static constexpr int W_ROW = BM;
-    static constexpr int WLO_ROW = BM + BN;
-    static constexpr int ALO_ROW = WLO_ROW + (SW ? BN : 0);
-    static constexpr int ROWS = ALO_ROW + (SA ? BM : 0);
-    static constexpr int HALVES = ROWS * BK;
-    static constexpr int LOADS = ROWS / ROWS_PER_ROUND;   // DMA instructions per wave per stage
-    static_assert(BM % ROWS_PER_ROUND == 0 && BN % ROWS_PER_ROUND == 0, "rows per round");
-    __device__ __forceinline__ static int swz(int row) { return (row / SWZ_DIV) % CPR; }
-};
-
-template <int BM, int BN, int BK, int NS, int MODE, int ACT, bool OUT_F16>
-struct DmaGemm {
-    using L = DmaLayout<BM, BN, BK, MODE>;
-    static constexpr bool SPLIT = MODE != 0;
-    static constexpr int WM = BM / 2, WN = BN / 2;
-    static constexpr int TM = WM / 32, TN = WN / 32;
-
-    const _Float16* __restrict__ A;
-    const _Float16* __restrict__ Alo;
-    const _Float16* __restrict__ W;
-    const _Float16* __restrict__ Wlo;
-    int64_t M, N, K, m0, n0, nk;
-    int wave, lane, wm, wn, lr, lg;
-    floatx16 acc[TM][TN];
-    floatx16 acc2[SPLIT ? TM : 1][SPLIT ? TN : 1];
-
-    // A stage's DMA instructions (this wave's), in order: the rounds of A,
-    // W, lo(W) (MODE & 1), lo(A) (MODE & 2). Each lane's byte offset
-    // into its operand at k = 0 is computed once (row clamped to the last
-    // valid one, logical chunk from the swizzle); a stage then only adds the
-    // wave-uniform k offset to the operand's base, in scalar registers.
-    static constexpr int RA = BM / L::ROWS_PER_ROUND, RW = BN / L::ROWS_PER_ROUND;
-    static constexpr int NDMA = L::LOADS;
-    static constexpr int KS = BK / 16;
-    static constexpr int NWLO = L::SW ? RW : 0;
-    static constexpr int op_of(int d) {
-        return d < RA ? 0 : (d < RA + RW ? 1 : (d < RA + RW + NWLO ? 2 : 3));
-    }
-    static constexpr int round_of(int d) {
-        return d < RA ? d : (d < RA + RW ? d - RA : (d < RA + RW + NWLO ? d - RA - RW : d - RA - RW - NWLO));
-    }
-    static constexpr int region_row(int op) {
-        return op == 0 ? L::A_ROW : (op == 1 ? L::W_ROW : (op == 2 ? L::WLO_ROW : L::ALO_ROW));
-    }
-    unsigned doff[NDMA];
-
-    __device__ __forceinline__ void init_offsets() {
-        const int sub = lane / L::CPR;      // row within this wave's instruction
-        const int pc = lane % L::CPR;       // physical chunk this lane fills
-        static_for<0, NDMA>([&](auto dd) {
-            constexpr int D = decltype(dd)::value;
-            constexpr int op = op_of(D);
-            constexpr bool is_a = op == 0 || op == 3;
-            const int r = round_of(D) * L::ROWS_PER_ROUND + wave * L::ROWS_PER_DMA + sub;
-            const int lc = pc ^ L::swz(r);  // logical chunk it holds
-            const int64_t nrows = is_a ? M : N;
-            int64_t gr = (is_a ? m0 : n0) + r;
-            gr = gr < nrows ? gr : nrows - 1;
-            doff[D] = static_cast<unsigned>((gr * K + lc * 8) * 2);
-        });
-    }
-
-    template <int D>
-    __device__ __forceinline__ void issue_one(_Float16* stage, int64_t kt) const {
-        constexpr int op = op_of(D);
-        const _Float16* src = op == 0 ? A : (op == 1 ? W : (op == 2 ? Wlo : Alo));
-        constexpr int row = region_row(op) + round_of(D) * L::ROWS_PER_ROUND;
-        dma16_off(src + kt * BK, doff[D], stage + (row + wave * L::ROWS_PER_DMA) * BK);
-    }
-
-    // DMAs [LO, HI) of tile kt into `stage`.
-    template <int LO, int HI>
-    __device__ __forceinline__ void issue_range(_Float16* stage, int64_t kt) const {
-        static_for<LO, HI>([&](auto dd) { issue_one<decltype(dd)::value>(stage, kt); });
-    }
-
-    // Fragment of row `row` (tile-local), 16-wide k step `ks`: the 8 halves of
-    // lane group lg, at the swizzled chunk.
-    __device__ __forceinline__ half8 frag(const _Float16* region, int row, int ks) const {
-        const int pc = (ks * 2 + lg) ^ L::swz(row);
-        return *reinterpret_cast<const half8*>(region + row * BK + pc * 8);
-    }
-
-    // Multiply the tile in `stage`; if `more`, issue tile kt_next into
-    // `next` meanwhile, one slice of its DMAs after each row of MFMAs, so the
-    // vector-memory issue (which stalls while the CU's load queue is full)
-    // runs under the matrix cores instead of ahead of them.
-    __device__ __forceinline__ void compute(const _Float16* stage, _Float16* next, int64_t kt_next,
-                                            bool more) {
-        constexpr int SLOTS = KS * TM;
-        static_for<0, KS>([&](auto kk) {
-            constexpr int ks = decltype(kk)::value;
-            half8 a[TM], b[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) a[i] = frag(stage + L::A_ROW * BK, wm * WM + i * 32 + lr, ks);
-#pragma unroll
-            for (int j = 0; j < TN; ++j) b[j] = frag(stage + L::W_ROW * BK, wn * WN + j * 32 + lr, ks);
-            static_for<0, TM>([&](auto ii) {
-                constexpr int i = decltype(ii)::value;
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], a[i], acc[i][j], 0, 0, 0);
-                constexpr int slot = ks * TM + i;
-                if (more) issue_range<slot * NDMA / SLOTS, (slot + 1) * NDMA / SLOTS>(next, kt_next);
-            });
-            if constexpr (L::SW) {
-                half8 bl[TN];
-#pragma unroll
-                for (int j = 0; j < TN; ++j) bl[j] = frag(stage + L::WLO_ROW * BK, wn * WN + j * 32 + lr, ks);
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bl[j], a[i], acc2[i][j], 0, 0, 0);
-            }
-            if constexpr (L::SA) {
-                half8 al[TM];
-#pragma unroll
-                for (int i = 0; i < TM; ++i) al[i] = frag(stage + L::ALO_ROW * BK, wm * WM + i * 32 + lr, ks);
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], al[i], acc2[i][j], 0, 0, 0);
-            }
-        });
-    }
-
-    // Wait until tile kt's DMAs (this wave's) have landed. Younger tiles
-    // already issued: min(NS - 2, nk - 1 - kt); each is L::LOADS instructions.
-    template <int Y>
-    __device__ __forceinline__ void wait_younger(int64_t younger) const {
-        if constexpr (Y == 0) {
-            wait_vmcnt<0>();
-        } else {
-            if (younger >= Y) { wait_vmcnt<Y * L::LOADS>(); return; }
-            wait_younger<Y - 1>(younger);
-        }
-    }
-    __device__ __forceinline__ void wait_tile(int64_t kt) const {
-        wait_younger<NS - 2>(nk - 1 - kt);
-    }
-};
-
-template <int BM, int BN, int BK, int NS, int MODE, int ACT, bool OUT_F16>
-__global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
-    const _Float16* __restrict__ A, const _Float16* __restrict__ Alo,
-    const _Float16* __restrict__ W, const _Float16* __restrict__ Wlo,
-    const float* __restrict__ bias, const float* __restrict__ R, void* __restrict__ C, int64_t M,
-    int64_t N, int64_t K) {
-    using G = DmaGemm<BM, BN, BK, NS, MODE, ACT, OUT_F16>;
-    using L = typename G::L;
-    static_assert(NS >= 2 && NS <= 8, "2 to 8 stages");
-    static_assert((NS - 2) * L::LOADS < 64, "vmcnt is 6 bits");
-    constexpr int SZ = L::HALVES;
-
-    // One __shared__ array per stage (see the header comment).
-    __shared__ __attribute__((aligned(1024))) _Float16 st0[SZ];
-    __shared__ __attribute__((aligned(1024))) _Float16 st1[SZ];
-    __shared__ __attribute__((aligned(1024))) _Float16 st2[NS > 2 ? SZ : 8];
-    __shared__ __attribute__((aligned(1024))) _Float16 st3[NS > 3 ? SZ : 8];
-    __shared__ __attribute__((aligned(1024))) _Float16 st4[NS > 4 ? SZ : 8];
-    __shared__ __attribute__((aligned(1024))) _Float16 st5[NS > 5 ? SZ : 8];
-    __shared__ __attribute__((aligned(1024))) _Float16 st6[NS > 6 ? SZ : 8];
-    __shared__ __attribute__((aligned(1024))) _Float16 st7[NS > 7 ? SZ : 8];
-
-    G g;
-    g.A = A; g.Alo = Alo; g.W = W; g.Wlo = Wlo;
-    g.M = M; g.N = N; g.K = K;
-    g.lane = threadIdx.x & 63;
-    g.wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    g.wm = g.wave >> 1;
-    g.wn = g.wave & 1;
-    g.lr = g.lane & 31;
-    g.lg = g.lane >> 5;
-    int64_t mt, nt;
-    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, mt, nt);
-    g.m0 = mt * BM;
-    g.n0 = nt * BN;
-    g.nk = K / BK;
-    g.init_offsets();
-#pragma unroll
-    for (int i = 0; i < G::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < G::TN; ++j) {
-            g.acc[i][j] = floatx16{};
-            if constexpr (G::SPLIT) g.acc2[i][j] = floatx16{};
-        }
-
-    auto stage = [&](auto s) -> _Float16* {
-        constexpr int S = decltype(s)::value;
-        if constexpr (S == 0) return st0;
-        else if constexpr (S == 1) return st1;
-        else if constexpr (S == 2) return st2;
-        else if constexpr (S == 3) return st3;
-        else if constexpr (S == 4) return st4;
-        else if constexpr (S == 5) return st5;
-        else if constexpr (S == 6) return st6;
-        else return st7;
-    };
-
-    // The tile's bias columns, staged in LDS before the K loop (the loop's
-    // barriers publish them): read in the epilogue from LDS, they do not wait
-    // behind the epilogue's own global stores the way a global load would.
-    __shared__ __attribute__((aligned(16))) float sbias[BN];
-    for (int c = threadIdx.x; c < BN; c += kThreads) {
-        const int64_t col = g.n0 + c;
-        sbias[c] = col < N ? bias[col] : 0.f;
-    }
-
-    // Prologue: tiles 0 .. NS-2 in flight.
-    auto prologue = [&](auto s) {
-        constexpr int S = decltype(s)::value;
-        if constexpr (S < NS - 1) {
-            if (S < g.nk) g.template issue_range<0, G::NDMA>(stage(s), S);
-        }
-    };
-    prologue(std::integral_constant<int, 0>{});
-    prologue(std::integral_constant<int, 1>{});
-    prologue(std::integral_constant<int, 2>{});
-    prologue(std::integral_constant<int, 3>{});
-    prologue(std::integral_constant<int, 4>{});
-    prologue(std::integral_constant<int, 5>{});
-    prologue(std::integral_constant<int, 6>{});
-
-    // One step: wait for tile kt (in stage S), barrier (everyone's DMAs for kt
-    // landed, everyone done reading the stage tile kt + NS - 1 will reuse),
-    // multiply tile kt while issuing tile kt + NS - 1 into stage
-    // (S + NS - 1) % NS.
-    auto step = [&](auto s, int64_t kt) {
-        constexpr int S = decltype(s)::value;
-        if constexpr (S < NS) {
-            constexpr int NEXT = (S + NS - 1) % NS;
-            g.wait_tile(kt);
-            stage_barrier();
-            g.compute(stage(s), stage(std::integral_constant<int, NEXT>{}), kt + NS - 1,
-                      kt + NS - 1 < g.nk);
-        }
-    };
-
-    int64_t kt = 0;
-    for (; kt + NS <= g.nk; kt += NS) {
-        step(std::integral_constant<int, 0>{}, kt);
-        step(std::integral_constant<int, 1>{}, kt + 1);
-        step(std::integral_constant<int, 2>{}, kt + 2);
-        step(std::integral_constant<int, 3>{}, kt + 3);
-        step(std::integral_constant<int, 4>{}, kt + 4);
-        step(std::integral_constant<int, 5>{}, kt + 5);
-        step(std::integral_constant<int, 6>{}, kt + 6);
-        step(std::integral_constant<int, 7>{}, kt + 7);
-    }
-    // Remainder: fewer than NS tiles, in stages 0, 1, ...
-    if (kt < g.nk) step(std::integral_constant<int, 0>{}, kt);
-    if (kt + 1 < g.nk) step(std::integral_constant<int, 1>{}, kt + 1);
-    if (kt + 2 < g.nk) step(std::integral_constant<int, 2>{}, kt + 2);
-    if (kt + 3 < g.nk) step(std::integral_constant<int, 3>{}, kt + 3);
-    if (kt + 4 < g.nk) step(std::integral_constant<int, 4>{}, kt + 4);
-    if (kt + 5 < g.nk) step(std::integral_constant<int, 5>{}, kt + 5);
-    if (kt + 6 < g.nk) step(std::integral_constant<int, 6>{}, kt + 6);
-
-    // Epilogue. The MFMAs were issued as W x A^T, so each 32x32 accumulator
-    // holds a tile of C^T: lane l owns C row (l % 32) of the tile, and
-    // registers 4g .. 4g+3 hold the four consecutive C columns
-    // 8g + 4 (l / 32) + 0..3 -- one 16-byte (fp32) or 8-byte (fp16) store.
-    const bool vec_ok = (N & 3) == 0;
-#pragma unroll
-    for (int i = 0; i < G::TM; ++i) {
-        const int64_t row = g.m0 + g.wm * G::WM + i * 32 + g.lr;
-        if (row >= M) continue;
-        float* crow32 = static_cast<float*>(C) + row * N;
-        _Float16* crow16 = static_cast<_Float16*>(C) + row * N;
-#pragma unroll
-        for (int j = 0; j < G::TN; ++j) {
-#pragma unroll
-            for (int grp = 0; grp < 4; ++grp) {
-                const int cl = g.wn * G::WN + j * 32 + 8 * grp + 4 * g.lg;  // tile-local column
-                const int64_t col = g.n0 + cl;
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float a = g.acc[i][j][4 * grp + e];
-                    if constexpr (G::SPLIT) a += g.acc2[i][j][4 * grp + e] * kLoUnscale;
-                    a += sbias[cl + e];
-                    if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
-                    v[e] = a;
-                }
-                if constexpr (!OUT_F16) {
-                    // residual stream: out = R + act(x W^T + b), the add the
-                    // following LayerNorm would otherwise do (same fp32 sum)
-                    if (R != nullptr) {
-                        const float* rrow = R + row * N + col;
-                        if (vec_ok && col + 4 <= N) {
-                            const float4 r4 = *reinterpret_cast<const float4*>(rrow);
-                            v[0] = r4.x + v[0]; v[1] = r4.y + v[1];
-                            v[2] = r4.z + v[2]; v[3] = r4.w + v[3];
-                        } else {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                if (col + e < N) v[e] = rrow[e] + v[e];
-                        }
-                    }
-                }
-                if (vec_ok && col + 4 <= N) {
-                    if constexpr (OUT_F16) {
-                        half4 h;
-                        h[0] = to_half(v[0]); h[1] = to_half(v[1]);
-                        h[2] = to_half(v[2]); h[3] = to_half(v[3]);
-                        *reinterpret_cast<half4*>(crow16 + col) = h;
-                    } else {
-                        *reinterpret_cast<float4*>(crow32 + col) = make_float4(v[0], v[1], v[2], v[3]);
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        if (col + e < N) {
-                            if constexpr (OUT_F16) crow16[col + e] = to_half(v[e]);
-                            else crow32[col + e] = v[e];
-                        }
-                    }
-                }
-            }
-        }
-    }
-}
-
-struct DmaArgs {
-    const _Float16* A;
-    const _Float16* Alo;
-    const _Float16* W;
-    const _Float16* Wlo;
-    const float* bias;
-    const float* R;      // nullable fp32 [M, N] residual added to an fp32 output
-    void* C;
-    int64_t M, N, K;
-    hipStream_t stream;
-};
-
-template <int BM, int BN, int BK, int NS, int MODE, int ACT, bool OUT_F16>
-void launch_dma(const DmaArgs& a) {
-    const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, MODE, ACT, OUT_F16>),
-                       dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, a.stream, a.A,
-                       a.Alo, a.W, a.Wlo, a.bias, a.R, a.C, a.M, a.N, a.K);
-}
-
-// Tile ids (dotl_linear's `tile`): 0 128x128, 1 256x128, 2 64x64, 3 256x256,
-// 4 128x64. K tiles of 32; stage counts fill <= 144 KiB of LDS.
-template <int MODE, int ACT, bool OUT_F16>
-bool dispatch_tile(const DmaArgs& a, int tile) {
-    // Stage depths are chosen by operand planes a stage holds: 2 + split ones.
-    constexpr int PASSES = 1 + (MODE & 1) + ((MODE >> 1) & 1);
-    switch (tile) {
-        case 0:   // stage: 256 / 384 / 512 rows x 64 B = 16 / 24 / 32 KiB
-            if constexpr (PASSES == 1) launch_dma<128, 128, 32, 8, MODE, ACT, OUT_F16>(a);
-            else if constexpr (PASSES == 2) launch_dma<128, 128, 32, 6, MODE, ACT, OUT_F16>(a);
-            else launch_dma<128, 128, 32, 4, MODE, ACT, OUT_F16>(a);
-            return true;
-        case 1:   // 384 rows: 24 KiB
-            if constexpr (PASSES == 1) { launch_dma<256, 128, 32, 6, MODE, ACT, OUT_F16>(a); return true; }
-            return false;
-        case 2:   // 128 / 192 / 256 rows
-            if constexpr (PASSES == 1) launch_dma<64, 64, 32, 8, MODE, ACT, OUT_F16>(a);
-            else launch_dma<64, 64, 32, 8, MODE, ACT, OUT_F16>(a);
-            return true;
-        case 3:   // 512 rows: 32 KiB
-            if constexpr (PASSES == 1) { launch_dma<256, 256, 32, 4, MODE, ACT, OUT_F16>(a); return true; }
-            return false;
-        case 4:   // 192 / 320 / 384 rows
-            if constexpr (PASSES == 1) launch_dma<128, 64, 32, 8, MODE, ACT, OUT_F16>(a);
-            else if constexpr (PASSES == 2) launch_dma<128, 64, 32, 7, MODE, ACT, OUT_F16>(a);
-            else launch_dma<128, 64, 32, 6, MODE, ACT, OUT_F16>(a);
-            return true;
-        // Shallow pipelines whose LDS (<= 72 KiB) lets two workgroups share a
-        // CU, i.e. two waves per SIMD, the co-resident one hiding latency.
-        case 5:
-            if constexpr (PASSES == 1) launch_dma<128, 128, 32, 4, MODE, ACT, OUT_F16>(a);
-            else if constexpr (PASSES == 2) launch_dma<128, 128, 32, 3, MODE, ACT, OUT_F16>(a);
-            else launch_dma<128, 128, 32, 2, MODE, ACT, OUT_F16>(a);
-            return true;
-        case 6:
-            if constexpr (PASSES == 1) { launch_dma<256, 128, 32, 3, MODE, ACT, OUT_F16>(a); return true; }
-            return false;
-        case 7:
-            if constexpr (PASSES == 1) launch_dma<128, 64, 32, 4, MODE, ACT, OUT_F16>(a);
-            else launch_dma<128, 64, 32, 3, MODE, ACT, OUT_F16>(a);
-            return true;
-        case 8:
-            launch_dma<64, 64, 32, 4, MODE, ACT, OUT_F16>(a);
-            return true;
-        // BK = 64: each row of a stage is one whole 128-byte line, so every
-        // DMA instruction reads 8 full lines instead of 16 half lines.
-        case 9:   // 512 rows x 128 B = 64 KiB a stage
-            if constexpr (PASSES == 1) { launch_dma<256, 256, 64, 2, MODE, ACT, OUT_F16>(a); return true; }
-            return false;
-        case 10:  // 256 / 384 / 512 rows: 32 / 48 / 64 KiB
-            if constexpr (PASSES == 1) launch_dma<128, 128, 64, 4, MODE, ACT, OUT_F16>(a);
-            else if constexpr (PASSES == 2) launch_dma<128, 128, 64, 3, MODE, ACT, OUT_F16>(a);
-            else launch_dma<128, 128, 64, 2, MODE, ACT, OUT_F16>(a);
-            return true;
-        case 11:  // 384 rows: 48 KiB
-            if constexpr (PASSES == 1) { launch_dma<256, 128, 64, 3, MODE, ACT, OUT_F16>(a); return true; }
-            return false;
-        case 12:  // two workgroups a CU
-            if constexpr (PASSES == 1) { launch_dma<128, 128, 64, 2, MODE, ACT, OUT_F16>(a); return true; }
-            return false;
-        case 13:  // 192 / 320 / 384 rows
-            if constexpr (PASSES == 1) launch_dma<128, 64, 64, 3, MODE, ACT, OUT_F16>(a);
-            else launch_dma<128, 64, 64, 2, MODE, ACT, OUT_F16>(a);
-            return true;
-        // 192x128: fewer, larger tiles where 128-row tiles leave a short
-        // second wave of workgroups. 320 / 512 rows: 40 / 64 KiB a stage
-        // (three passes would not fit two stages).
-        case 14:
-            if constexpr (PASSES == 1) { launch_dma<192, 128, 64, 3, MODE, ACT, OUT_F16>(a); return true; }
-            else if constexpr (PASSES == 2) { launch_dma<192, 128, 64, 2, MODE, ACT, OUT_F16>(a); return true; }
-            return false;
-    }
-    return false;
-}
-
-}  // namespace
+using gemm_dma::DmaArgs;
+using gemm_dma::dispatch_tile;
 
 // Tile choice, from sweeps of every GEMM of the five layer configs on MI355X
 // (passes = planes multiplied: 1 + split x + split W):

@@ -69,12 +69,14 @@ def library_path() -> str:
     return _LIB_PATH
 
 
-def build(verbose: bool = False, jobs: int = 8) -> str:
+def build(verbose: bool = False, jobs: int = 8, force: bool = True) -> str:
     """Compile libdotl_hip.so for gfx950 with the Makefile in csrc/ (hipcc).
 
-    Needs no GPU: hipcc cross-compiles. Returns the library path.
+    Needs no GPU: hipcc cross-compiles. `force` (the default) recompiles every
+    source (make -B, ~4 minutes on 8 cores), so a build check never passes on
+    objects left from an earlier build. Returns the library path.
     """
-    cmd = ["make", "-C", _CSRC, f"-j{jobs}"]
+    cmd = ["make", "-C", _CSRC, f"-j{jobs}"] + (["-B"] if force else [])
     res = subprocess.run(cmd, capture_output=True, text=True)
     if verbose or res.returncode != 0:
         print(res.stdout)
