@@ -453,7 +453,9 @@ def _main(out):
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (--gpus {args.gpus} "
-              f"was asked for). The layer shards by batch with no exchange; see DESIGN.md.",
+              f"was asked for). The layer shards by batch: replicated weights, each rank a slice "
+              f"of the batch, nothing exchanged, so one GPU's share at its real shape is what "
+              f"this measures.",
               file=sys.stderr)
         return 2
     if args.profile_ops:
