@@ -39,11 +39,15 @@
 //     by tiles that need it (boundary, diagonal, or masked tiles).
 #include "attention_params.h"
 
+#include <algorithm>
+#include <type_traits>
+
 namespace dotl {
 
 int attention_fp16_default();
 int attention_cp_async_mode();
 void attention_pipeline(int* nw, int* ns);
+void attention_split_knobs(int* enabled, int* forced);
 
 namespace {
 
@@ -51,12 +55,6 @@ constexpr int kBN = 64;    // keys per tile
 constexpr int kVPad = 8;   // halves of padding per V^T row
 constexpr int kKPad = 8;   // halves of padding per K row
 
-template <bool IN_F32>
-struct Elem;
-template <>
-struct Elem<false> { using T = _Float16; };
-template <>
-struct Elem<true> { using T = float; };
 
 // MFMA operand type: fp16, or bf16 (fp32 tensors with precision=bf16).
 template <bool BF16>
@@ -82,12 +80,13 @@ struct Ops<true> {
     }
 };
 
-// Load 8 consecutive head-dim elements as the operand type (narrowing fp32
-// with round-to-nearest-even).
-template <bool IN_F32, bool BF16>
-__device__ __forceinline__ typename Ops<BF16>::v8 load8(const typename Elem<IN_F32>::T* p) {
+// Load 8 consecutive head-dim elements of a TIN tensor as the operand type
+// (narrowing fp32 with round-to-nearest-even; 16-bit tensors are read as
+// they are, in their own operand type).
+template <typename TIN, bool BF16>
+__device__ __forceinline__ typename Ops<BF16>::v8 load8(const TIN* p) {
     using O = Ops<BF16>;
-    if constexpr (IN_F32) {
+    if constexpr (sizeof(TIN) == 4) {
         const float4 a = *reinterpret_cast<const float4*>(p);
         const float4 b = *reinterpret_cast<const float4*>(p + 4);
         typename O::v8 h;
@@ -97,14 +96,15 @@ __device__ __forceinline__ typename Ops<BF16>::v8 load8(const typename Elem<IN_F
         h[6] = static_cast<typename O::E>(b.z); h[7] = static_cast<typename O::E>(b.w);
         return h;
     } else {
-        static_assert(!BF16, "fp16 tensors contract in fp16");
-        return *reinterpret_cast<const half8*>(p);
+        static_assert(std::is_same<TIN, typename O::E>::value,
+                      "16-bit tensors contract in their own type");
+        return *reinterpret_cast<const typename O::v8*>(p);
     }
 }
 
-template <int HD, int NW, bool IN_F32, bool OUT_F32, bool BF16>
+template <int HD, int NW, typename TIN, typename TOUT, bool BF16>
 __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
-    using T = typename Elem<IN_F32>::T;
+    using T = TIN;
     using O = Ops<BF16>;
     using E = typename O::E;
     using v8 = typename O::v8;
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         qf[ks] = v8{};
-        if (my_q < S) qf[ks] = load8<IN_F32, BF16>(qbase + static_cast<int64_t>(my_q) * p.ss + ks * 16 + lg * 8);
+        if (my_q < S) qf[ks] = load8<TIN, BF16>(qbase + static_cast<int64_t>(my_q) * p.ss + ks * 16 + lg * 8);
     }
 
     const bool has_mask = p.mask != nullptr;
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
             const int col = (c % (HD / 8)) * 8;
             rk[i] = v8{};
             if (c < KCH && key0 + row < S)
-                rk[i] = load8<IN_F32, BF16>(kbase + static_cast<int64_t>(key0 + row) * p.ss + col);
+                rk[i] = load8<TIN, BF16>(kbase + static_cast<int64_t>(key0 + row) * p.ss + col);
         }
 #pragma unroll
         for (int i = 0; i < VPER; ++i) {
@@ -212,8 +212,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
             rv1[i] = v8{};
             if (it < VIT) {
                 const int k0 = key0 + 2 * kp;
-                if (k0 < S) rv0[i] = load8<IN_F32, BF16>(vbase + static_cast<int64_t>(k0) * p.ss + ch * 8);
-                if (k0 + 1 < S) rv1[i] = load8<IN_F32, BF16>(vbase + static_cast<int64_t>(k0 + 1) * p.ss + ch * 8);
+                if (k0 < S) rv0[i] = load8<TIN, BF16>(vbase + static_cast<int64_t>(k0) * p.ss + ch * 8);
+                if (k0 + 1 < S) rv1[i] = load8<TIN, BF16>(vbase + static_cast<int64_t>(k0 + 1) * p.ss + ch * 8);
             }
         }
         if (key_only_mask && threadIdx.x < kBN) {
@@ -375,47 +375,38 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnParams p) {
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) {
                 const int d = 32 * j + 8 * rb + 4 * lg;
-                if constexpr (OUT_F32) {
-                    float4 w4 = make_float4(o[j][4 * rb] * inv, o[j][4 * rb + 1] * inv,
-                                            o[j][4 * rb + 2] * inv, o[j][4 * rb + 3] * inv);
-                    *reinterpret_cast<float4*>(static_cast<float*>(p.out) + obase + d) = w4;
-                } else {
-                    half4 w4;
-                    w4[0] = to_half(o[j][4 * rb] * inv);
-                    w4[1] = to_half(o[j][4 * rb + 1] * inv);
-                    w4[2] = to_half(o[j][4 * rb + 2] * inv);
-                    w4[3] = to_half(o[j][4 * rb + 3] * inv);
-                    *reinterpret_cast<half4*>(static_cast<_Float16*>(p.out) + obase + d) = w4;
-                }
+                store4f(static_cast<TOUT*>(p.out) + obase + d,
+                        make_float4(o[j][4 * rb] * inv, o[j][4 * rb + 1] * inv,
+                                    o[j][4 * rb + 2] * inv, o[j][4 * rb + 3] * inv));
             }
         }
     }
 }
 
-template <int HD, int NW, bool IN_F32, bool OUT_F32, bool BF16>
+template <int HD, int NW, typename TIN, typename TOUT, bool BF16>
 void launch_attn(const AttnParams& p, hipStream_t stream) {
     const int64_t blocks = static_cast<int64_t>(p.nqb) * p.B * p.H;
-    hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, IN_F32, OUT_F32, BF16>), dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, TIN, TOUT, BF16>), dim3(static_cast<unsigned>(blocks)),
                        dim3(NW * 64), 0, stream, p);
 }
 
 int waves_for(int S) { return attn_waves_for(S); }
 
-template <int HD, bool IN_F32, bool OUT_F32, bool BF16>
+template <int HD, typename TIN, typename TOUT, bool BF16>
 void launch_nw(const AttnParams& p, hipStream_t stream) {
     switch (waves_for(p.S)) {
-        case 1: launch_attn<HD, 1, IN_F32, OUT_F32, BF16>(p, stream); break;
-        case 2: launch_attn<HD, 2, IN_F32, OUT_F32, BF16>(p, stream); break;
-        default: launch_attn<HD, 4, IN_F32, OUT_F32, BF16>(p, stream); break;
+        case 1: launch_attn<HD, 1, TIN, TOUT, BF16>(p, stream); break;
+        case 2: launch_attn<HD, 2, TIN, TOUT, BF16>(p, stream); break;
+        default: launch_attn<HD, 4, TIN, TOUT, BF16>(p, stream); break;
     }
 }
 
-template <bool IN_F32, bool OUT_F32, bool BF16>
+template <typename TIN, typename TOUT, bool BF16>
 bool launch_hd(int hd, const AttnParams& p, hipStream_t stream) {
     switch (hd) {
-        case 32: launch_nw<32, IN_F32, OUT_F32, BF16>(p, stream); return true;
-        case 64: launch_nw<64, IN_F32, OUT_F32, BF16>(p, stream); return true;
-        case 128: launch_nw<128, IN_F32, OUT_F32, BF16>(p, stream); return true;
+        case 32: launch_nw<32, TIN, TOUT, BF16>(p, stream); return true;
+        case 64: launch_nw<64, TIN, TOUT, BF16>(p, stream); return true;
+        case 128: launch_nw<128, TIN, TOUT, BF16>(p, stream); return true;
         default: return false;
     }
 }
@@ -444,42 +435,73 @@ const char* precision_name(int prec) {
 }  // namespace
 }  // namespace dotl
 
-extern "C" int dotl_attention_forward(const void* q, const void* k, const void* v, int dtype,
-                                      const int64_t* qkv_strides, const uint8_t* mask,
-                                      const int64_t* mask_strides, void* out, int out_dtype,
-                                      int out_layout, int B, int H, int S, int head_dim,
-                                      int is_causal, double scale, int impl, int precision,
-                                      const int32_t* cu_seqlens, void* stream) {
-    using namespace dotl;
-    clear_error();
-    DOTL_REQUIRE(out_layout == 0 || out_layout == 1,
-                 "fused_attention_forward: out_layout must be 0 ([B,H,S,head_dim]) or 1 "
-                 "([B,S,H*head_dim])");
-    DOTL_REQUIRE(impl >= 0 && impl <= 3,
-                 "fused_attention_forward: impl must be 0 (auto), 1 (scalar), 2 (wmma) or 3 (tile)");
-    DOTL_REQUIRE(precision >= 0 && precision <= 4,
-                 "fused_attention_forward: precision must be 0 (auto), 1 (fp32), 2 (tf32), "
-                 "3 (fp16) or 4 (bf16)");
-    DOTL_REQUIRE(dtype == DOTL_F16 || dtype == DOTL_F32,
-                 "fused_attention_forward: q/k/v must be float16 or float32");
-    DOTL_REQUIRE(out_dtype == DOTL_F16 || out_dtype == DOTL_F32,
-                 "fused_attention_forward: out must be float16 or float32");
-    DOTL_REQUIRE(B >= 0 && H >= 0 && S >= 0 && head_dim > 0,
-                 "fused_attention_forward: negative extent");
-    DOTL_REQUIRE(qkv_strides != nullptr, "fused_attention_forward: strides required");
+namespace dotl {
+namespace {
 
-    // The impl x precision vocabulary of the reference
-    // (reference csrc/attention_dispatch.cuh:219-304, attention_wmma.cuh:2043-2084):
-    //   * scalar (impl 1) is the exact fp32 kernel and has only fp32;
-    //   * wmma (impl 2) has no fp32. fp16 tensors contract in fp16 whatever the
-    //     precision; fp32 tensors narrow to the requested type, "auto" meaning
-    //     the process-wide fp16 knob (on: fp16, off: tf32). gfx950 has no tf32
-    //     matrix instruction, so a forced wmma declines tf32;
-    //   * auto (impl 0): fp32 -> scalar; otherwise the MFMA kernel where it
-    //     covers the head_dim and arithmetic, else the scalar kernel (whose
-    //     fp32 arithmetic is at least as precise as the request);
-    //   * "tile" is an NVIDIA programming model with no counterpart here and
-    //     always reports unavailable.
+// What one call will run: the kernel family and, for the LDS-DMA kernel,
+// its workgroup shape and key-range split. Decided from the arguments alone
+// (no device access), so dotl_attention_split_plan and the launch agree.
+struct AttnPlan {
+    bool use_scalar = false;
+    int mfma_prec = 3;      // 3 fp16, 4 bf16, 2 tf32 (none on gfx950)
+    bool dma = false;       // the LDS-DMA kernel (fp16 q/k/v)
+    int nw = 4, ns = 0;
+    int splits = 1;
+    int tiles_per_split = 0;
+};
+
+// Split-KV for the LDS-DMA kernel (reference csrc/attention_wmma.cuh:706-759
+// decides its split count from occupancy too). A grid of fewer workgroups
+// than the 256 CUs can hold two of leaves CUs idle for the whole kernel:
+// then the key range is cut into splits of at least two 64-key tiles, up to
+// 16, so the grid reaches ~512 workgroups; a combine pass merges them.
+// `requested`: 0 the knobs' choice (forced count, else this heuristic,
+// else none when disabled), 1 none, n > 1 that many (capped by the tiles).
+int split_count(const AttnPlan& plan, int B, int H, int S, bool masked, int requested) {
+    if (!plan.dma || (S <= 32 && requested <= 1)) return 1;
+    const int nkt = (S + 63) / 64;
+    int want = requested;
+    if (want == 0) {
+        int enabled = 1, forced = 0;
+        attention_split_knobs(&enabled, &forced);
+        if (!enabled) return 1;
+        if (forced > 0) {
+            want = forced;
+        } else {
+            const int nqb = masked ? (S + 127) / 128 : (S + 32 * plan.nw - 1) / (32 * plan.nw);
+            const int64_t blocks = static_cast<int64_t>(nqb) * B * H;
+            if (blocks >= 256) return 1;
+            want = static_cast<int>((512 + blocks - 1) / blocks);
+            want = std::min(want, std::min(16, nkt / 2));
+        }
+    }
+    if (want <= 1) return 1;
+    want = std::min(want, nkt);
+    const int per = (nkt + want - 1) / want;
+    return (nkt + per - 1) / per;
+}
+
+int tiles_per_split(int S, int splits) {
+    const int nkt = (S + 63) / 64;
+    return (nkt + splits - 1) / splits;
+}
+
+// Validates the impl x precision request and picks the kernel (the
+// reference's vocabulary, csrc/attention_dispatch.cuh:219-304,
+// attention_wmma.cuh:2043-2084):
+//   * scalar (impl 1) is the exact fp32 kernel and has only fp32;
+//   * wmma (impl 2) has no fp32. fp16 tensors contract in fp16 whatever the
+//     precision; fp32 tensors narrow to the requested type, "auto" meaning
+//     the process-wide fp16 knob (on: fp16, off: tf32). gfx950 has no tf32
+//     matrix instruction, so a forced wmma declines tf32; bf16 tensors
+//     contract in bf16;
+//   * auto (impl 0): fp32 -> scalar; otherwise the MFMA kernel where it
+//     covers the head_dim and arithmetic, else the scalar kernel (whose
+//     fp32 arithmetic is at least as precise as the request);
+//   * "tile" is an NVIDIA programming model with no counterpart here and
+//     always reports unavailable.
+// Returns DOTL_OK with `plan` filled, or the error/decline code (message set).
+int plan_attention(int dtype, int head_dim, int S, int impl, int precision, AttnPlan& plan) {
     if (impl == 3) {
         set_error("fused_attention_forward: impl=3 (tile) is not available in this build: the "
                   "tile programming model has no gfx950 counterpart");
@@ -496,16 +518,16 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
                   precision_name(precision) + " arithmetic. It supports: fp32.");
         return DOTL_E_UNSUPPORTED;
     }
-    // The MFMA arithmetic this call would get: 3 fp16, 4 bf16, 2 tf32 (none).
-    int mfma_prec = 3;
+    plan.mfma_prec = 3;
     if (dtype == DOTL_F32) {
-        mfma_prec = precision == 0 ? (attention_fp16_default() ? 3 : 2) : precision;
+        plan.mfma_prec = precision == 0 ? (attention_fp16_default() ? 3 : 2) : precision;
+    } else if (dtype == DOTL_BF16) {
+        plan.mfma_prec = 4;
     }
     const bool mfma_hd = head_dim == 32 || head_dim == 64 || head_dim == 128;
-    const bool mfma_ok = mfma_hd && (mfma_prec == 3 || mfma_prec == 4);
-    bool use_scalar;
+    const bool mfma_ok = mfma_hd && (plan.mfma_prec == 3 || plan.mfma_prec == 4);
     if (impl == 1 || (impl == 0 && precision == 1)) {
-        use_scalar = true;
+        plan.use_scalar = true;
     } else if (impl == 2) {
         if (!mfma_ok) {
             char buf[320];
@@ -513,16 +535,16 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
                           "fused_attention_forward: impl=2 (wmma), precision=%s does not cover "
                           "head_dim=%d%s; the MFMA kernel covers head_dim in {32, 64, 128} with "
                           "fp16 or bf16 operands",
-                          precision_name(mfma_prec), head_dim,
-                          mfma_prec == 2 ? " (gfx950 has no tf32 matrix instruction)" : "");
+                          precision_name(plan.mfma_prec), head_dim,
+                          plan.mfma_prec == 2 ? " (gfx950 has no tf32 matrix instruction)" : "");
             set_error(buf);
             return DOTL_DECLINED;
         }
-        use_scalar = false;
+        plan.use_scalar = false;
     } else {
-        use_scalar = !mfma_ok;
+        plan.use_scalar = !mfma_ok;
     }
-    if (use_scalar && head_dim > kMaxScalarHeadDim) {
+    if (plan.use_scalar && head_dim > kMaxScalarHeadDim) {
         char buf[256];
         std::snprintf(buf, sizeof(buf),
                       "fused_attention_forward: impl=%d (%s), precision=%s does not cover "
@@ -532,20 +554,113 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
         set_error(buf);
         return DOTL_DECLINED;
     }
+    plan.nw = waves_for(S);
+    plan.ns = 0;
+    plan.dma = !plan.use_scalar && dtype == DOTL_F16 && attention_cp_async_mode() != 0;
+    if (plan.dma) {
+        // The pipelined kernel: 8 waves (256 queries) a workgroup for
+        // head_dim 128 from S = 2048, measured 4% faster there than 4.
+        if (head_dim == 128 && S >= 2048) plan.nw = 8;
+        int fnw = 0, fns = 0;
+        attention_pipeline(&fnw, &fns);
+        if (fnw == 1 || fnw == 2 || fnw == 4 || fnw == 8) plan.nw = fnw;
+        if (fns >= 1 && fns <= 4) plan.ns = fns;
+    }
+    return DOTL_OK;
+}
+
+}  // namespace
+}  // namespace dotl
+
+extern "C" int dotl_attention_split_plan(int B, int H, int S, int head_dim, int is_causal,
+                                         int dtype, int has_mask, int64_t rows, int impl,
+                                         int precision, int splits, int* splits_out,
+                                         int64_t* workspace_bytes_out) {
+    using namespace dotl;
+    (void)is_causal;
+    clear_error();
+    DOTL_REQUIRE(splits_out != nullptr && workspace_bytes_out != nullptr,
+                 "attention_split_plan: null output");
+    DOTL_REQUIRE(splits >= 0, "attention_split_plan: negative split count");
+    *splits_out = 1;
+    *workspace_bytes_out = 0;
+    AttnPlan plan;
+    const int rc = plan_attention(dtype, head_dim, S, impl, precision, plan);
+    if (rc != DOTL_OK) return rc;
+    const int n = split_count(plan, B, H, S, has_mask != 0, splits);
+    *splits_out = n;
+    *workspace_bytes_out = attn_split_workspace_bytes(rows, H, head_dim, n);
+    return DOTL_OK;
+}
+
+extern "C" int dotl_attention_forward(const void* q, const void* k, const void* v, int dtype,
+                                      const int64_t* qkv_strides, const uint8_t* mask,
+                                      const int64_t* mask_strides, void* out, int out_dtype,
+                                      int out_layout, int B, int H, int S, int head_dim,
+                                      int is_causal, double scale, int impl, int precision,
+                                      const int32_t* cu_seqlens, int64_t rows, int splits,
+                                      void* workspace, int64_t workspace_bytes, void* stream) {
+    using namespace dotl;
+    clear_error();
+    DOTL_REQUIRE(out_layout == 0 || out_layout == 1,
+                 "fused_attention_forward: out_layout must be 0 ([B,H,S,head_dim]) or 1 "
+                 "([B,S,H*head_dim])");
+    DOTL_REQUIRE(impl >= 0 && impl <= 3,
+                 "fused_attention_forward: impl must be 0 (auto), 1 (scalar), 2 (wmma) or 3 (tile)");
+    DOTL_REQUIRE(precision >= 0 && precision <= 4,
+                 "fused_attention_forward: precision must be 0 (auto), 1 (fp32), 2 (tf32), "
+                 "3 (fp16) or 4 (bf16)");
+    DOTL_REQUIRE(dtype == DOTL_F16 || dtype == DOTL_F32 || dtype == DOTL_BF16,
+                 "fused_attention_forward: q/k/v must be float16, bfloat16 or float32");
+    DOTL_REQUIRE(out_dtype == dtype || (dtype != DOTL_BF16 && out_dtype != DOTL_BF16 &&
+                                        (out_dtype == DOTL_F16 || out_dtype == DOTL_F32)),
+                 "fused_attention_forward: out must be float16 or float32 (bfloat16 for "
+                 "bfloat16 q/k/v)");
+    DOTL_REQUIRE(B >= 0 && H >= 0 && S >= 0 && head_dim > 0,
+                 "fused_attention_forward: negative extent");
+    DOTL_REQUIRE(qkv_strides != nullptr, "fused_attention_forward: strides required");
+    DOTL_REQUIRE(splits >= 0, "fused_attention_forward: negative split count");
+
+    AttnPlan plan;
+    const int prc = plan_attention(dtype, head_dim, S, impl, precision, plan);
+    if (prc != DOTL_OK) return prc;
     if (B == 0 || H == 0 || S == 0) return DOTL_OK;
+    DOTL_REQUIRE(cu_seqlens == nullptr || rows >= 0,
+                 "fused_attention_forward: packed sequences need their row count");
+
+    // Split-KV: the requested count resolved as dotl_attention_split_plan
+    // does; the partials live in the caller's workspace.
+    const int nsplit = split_count(plan, B, H, S, mask != nullptr, splits);
+    const int64_t part_rows = cu_seqlens != nullptr ? rows : static_cast<int64_t>(B) * S;
+    bool do_split = false;
+    if (nsplit > 1) {
+        const int64_t need = attn_split_workspace_bytes(part_rows, H, head_dim, nsplit);
+        if (workspace != nullptr && workspace_bytes >= need) {
+            do_split = part_rows > 0;
+        } else if (splits > 1) {
+            char buf[200];
+            std::snprintf(buf, sizeof(buf),
+                          "fused_attention_forward: %d key splits need %lld bytes of "
+                          "workspace, %lld given",
+                          nsplit, static_cast<long long>(need),
+                          static_cast<long long>(workspace_bytes));
+            set_error(buf);
+            return DOTL_E_INVALID;
+        }
+    }
     DOTL_REQUIRE(q && k && v && out, "fused_attention_forward: null pointer");
     DOTL_REQUIRE(mask == nullptr || mask_strides != nullptr,
                  "fused_attention_forward: mask strides required with a mask");
     DOTL_REQUIRE(cu_seqlens == nullptr || (mask == nullptr && out_layout == 1),
                  "fused_attention_forward: packed sequences (cu_seqlens) take no mask and "
                  "write the packed [rows, H*head_dim] layout (out_layout 1)");
-    const int64_t es = dtype == DOTL_F16 ? 2 : 4;
+    const int64_t es = dtype == DOTL_F32 ? 4 : 2;
     const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                             reinterpret_cast<uintptr_t>(v) |
                             static_cast<uintptr_t>(qkv_strides[0] * es) |
                             static_cast<uintptr_t>(qkv_strides[1] * es) |
                             static_cast<uintptr_t>(qkv_strides[2] * es);
-    DOTL_REQUIRE(use_scalar || align % 16 == 0,
+    DOTL_REQUIRE(plan.use_scalar || align % 16 == 0,
                  "fused_attention_forward: q/k/v rows must be 16-byte aligned for the MFMA kernel");
 
     AttnParams p{};
@@ -561,41 +676,54 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
     p.out_layout = out_layout;
     p.B = B; p.H = H; p.S = S;
     p.causal = is_causal ? 1 : 0;
-    int nw = waves_for(S), ns = 0;
-    if (dtype == DOTL_F16 && attention_cp_async_mode() != 0) {
-        // The pipelined kernel: 8 waves (256 queries) a workgroup for
-        // head_dim 128 from S = 2048, measured 4% faster there than 4.
-        if (head_dim == 128 && S >= 2048) nw = 8;
-        int fnw = 0, fns = 0;
-        attention_pipeline(&fnw, &fns);
-        if (fnw == 1 || fnw == 2 || fnw == 4 || fnw == 8) nw = fnw;
-        if (fns >= 1 && fns <= 4) ns = fns;
-    }
-    p.nqb = use_scalar ? attn_scalar_query_blocks(S, head_dim) : (S + 32 * nw - 1) / (32 * nw);
+    p.splits = 1;
+    const int nw = plan.nw, ns = plan.ns;
+    p.nqb = plan.use_scalar ? attn_scalar_query_blocks(S, head_dim) : (S + 32 * nw - 1) / (32 * nw);
     DOTL_REQUIRE(static_cast<int64_t>(p.nqb) * B * H <= 0x7fffffff,
                  "fused_attention_forward: grid too large");
     p.scale_log2 = static_cast<float>(scale * 1.4426950408889634);
     const hipStream_t st = as_stream(stream);
 
+    if (do_split) {
+        DOTL_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+                     "fused_attention_forward: workspace must be 16-byte aligned");
+        DOTL_REQUIRE(static_cast<int64_t>(p.nqb) * B * H * nsplit <= 0x7fffffff,
+                     "fused_attention_forward: grid too large");
+        p.splits = nsplit;
+        p.tiles_per_split = tiles_per_split(S, nsplit);
+        p.part_rows = part_rows;
+        p.part_o = static_cast<float*>(workspace);
+        p.part_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) +
+                                              static_cast<int64_t>(nsplit) * part_rows * H *
+                                                  head_dim * 4);
+    }
+
     const bool in32 = dtype == DOTL_F32;
     const bool out32 = out_dtype == DOTL_F32;
     bool launched;
-    if (use_scalar) {
-        launched = launch_attn_scalar(p, head_dim, in32, out32, static_cast<float>(scale), st);
-    } else if (in32 && mfma_prec == 4) {
-        launched = out32 ? launch_hd<true, true, true>(head_dim, p, st)
-                         : launch_hd<true, false, true>(head_dim, p, st);
+    if (plan.use_scalar) {
+        launched = launch_attn_scalar(p, head_dim, dtype, out_dtype, static_cast<float>(scale), st);
+    } else if (dtype == DOTL_BF16) {
+        launched = launch_hd<__bf16, __bf16, true>(head_dim, p, st);
+    } else if (in32 && plan.mfma_prec == 4) {
+        launched = out32 ? launch_hd<float, float, true>(head_dim, p, st)
+                         : launch_hd<float, _Float16, true>(head_dim, p, st);
     } else if (in32) {
-        launched = out32 ? launch_hd<true, true, false>(head_dim, p, st)
-                         : launch_hd<true, false, false>(head_dim, p, st);
-    } else if (attention_cp_async_mode() != 0) {
+        launched = out32 ? launch_hd<float, float, false>(head_dim, p, st)
+                         : launch_hd<float, _Float16, false>(head_dim, p, st);
+    } else if (plan.dma) {
         // fp16 q/k/v: K/V tiles streamed into LDS asynchronously (the
         // reference's cp_async staging; mode 0 selects the register-staged
         // kernel below).
         launched = launch_attn_dma(p, head_dim, out32, nw, ns, st);
+        if (launched && p.splits > 1) {
+            const int rc = check_launch("fused_attention_forward");
+            if (rc != DOTL_OK) return rc;
+            launched = launch_attn_split_combine(p, head_dim, out32, st);
+        }
     } else {
-        launched = out32 ? launch_hd<false, true, false>(head_dim, p, st)
-                         : launch_hd<false, false, false>(head_dim, p, st);
+        launched = out32 ? launch_hd<_Float16, float, false>(head_dim, p, st)
+                         : launch_hd<_Float16, _Float16, false>(head_dim, p, st);
     }
     if (!launched) {
         set_error("fused_attention_forward: no kernel instance for this shape");

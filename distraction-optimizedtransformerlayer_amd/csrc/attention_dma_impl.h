@@ -106,7 +106,13 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
     const int lg = lane >> 5;
 
     const int bh_count = p.B * p.H;
-    const int id = blockIdx.x;
+    int id = blockIdx.x;
+    int split = 0;
+    if (p.splits > 1) {
+        const int per_split = p.nqb * bh_count;
+        split = id / per_split;
+        id -= split * per_split;
+    }
     int qb = id / bh_count;
     const int bh = id - qb * bh_count;
     if (p.causal) {
@@ -157,6 +163,14 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
 
     const int kend = p.causal ? min(S, q_wg0 + 32 * NW) : S;
     const int nkt = (kend + kKB - 1) / kKB;
+    // This workgroup's key tiles: all of them, or its split's share (empty
+    // for a split past the causal limit or the sequence end: the loops then
+    // run no tile and the partials record an empty row).
+    int kt_begin = 0, kt_end = nkt;
+    if (p.splits > 1) {
+        kt_begin = split * p.tiles_per_split;
+        kt_end = min(nkt, kt_begin + p.tiles_per_split);
+    }
 
     auto kst = [&](auto s) __attribute__((always_inline)) -> _Float16*  {
         constexpr int I = decltype(s)::value;
@@ -432,7 +446,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
     // Wait for tile kt's DMAs: younger tiles already issued are
     // min(NS - 2, nkt - 1 - kt), each L instructions.
     auto wait_tile = [&](int kt) __attribute__((always_inline)) {
-        const int younger = nkt - 1 - kt;
+        const int younger = kt_end - 1 - kt;
         if constexpr (NS >= 4) {
             if (younger >= 2) { wait_vmcnt<2 * L>(); return; }
         }
@@ -446,8 +460,8 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
         // One stage (short sequences: usually a single tile): load, wait,
         // multiply; a barrier before each refill.
 #pragma unroll 1
-        for (int kt = 0; kt < nkt; ++kt) {
-            if (kt > 0) stage_barrier();
+        for (int kt = kt_begin; kt < kt_end; ++kt) {
+            if (kt > kt_begin) stage_barrier();
             issue(kt, k0s, v0s);
             wait_vmcnt<0>();
             stage_barrier();
@@ -457,7 +471,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
     auto prologue = [&](auto s) __attribute__((always_inline)) {
         constexpr int I = decltype(s)::value;
         if constexpr (I < NS - 1) {
-            if (I < nkt) issue(I, kst(s), vst(s));
+            if (kt_begin + I < kt_end) issue(kt_begin + I, kst(s), vst(s));
         }
     };
     prologue(std::integral_constant<int, 0>{});
@@ -470,7 +484,7 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
             constexpr int NEXT = (I + NS - 1) % NS;
             wait_tile(kt);
             stage_barrier();
-            const bool refill = kt + NS - 1 < nkt;
+            const bool refill = kt + NS - 1 < kt_end;
             auto dma = [&](auto jj) __attribute__((always_inline)) {
                 if (refill)
                     issue_one(jj, kt + NS - 1, kst(std::integral_constant<int, NEXT>{}),
@@ -481,30 +495,49 @@ __global__ __launch_bounds__(NW * 64, NW >= 8 ? 1 : 2) void attn_dma_kernel(Attn
     };
     // Tiles every wave computes: all of them, or under the causal limit
     // those up to the first query of the workgroup.
-    const int nfree = p.causal ? min(nkt, (q_wg0 + 31) / kKB + 1) : nkt;
+    const int nfree = p.causal ? min(kt_end, (q_wg0 + 31) / kKB + 1) : kt_end;
     const std::false_type all_waves;
     const std::true_type some_waves;
-    int kt = 0;
+    int kt = kt_begin;
     for (; kt + NS <= nfree; kt += NS) {
         step(std::integral_constant<int, 0>{}, kt, all_waves);
         step(std::integral_constant<int, 1>{}, kt + 1, all_waves);
         step(std::integral_constant<int, 2>{}, kt + 2, all_waves);
         step(std::integral_constant<int, 3>{}, kt + 3, all_waves);
     }
-    for (; kt + NS <= nkt; kt += NS) {
+    for (; kt + NS <= kt_end; kt += NS) {
         step(std::integral_constant<int, 0>{}, kt, some_waves);
         step(std::integral_constant<int, 1>{}, kt + 1, some_waves);
         step(std::integral_constant<int, 2>{}, kt + 2, some_waves);
         step(std::integral_constant<int, 3>{}, kt + 3, some_waves);
     }
-    if (kt < nkt) step(std::integral_constant<int, 0>{}, kt, some_waves);
-    if (kt + 1 < nkt) step(std::integral_constant<int, 1>{}, kt + 1, some_waves);
-    if (kt + 2 < nkt) step(std::integral_constant<int, 2>{}, kt + 2, some_waves);
+    if (kt < kt_end) step(std::integral_constant<int, 0>{}, kt, some_waves);
+    if (kt + 1 < kt_end) step(std::integral_constant<int, 1>{}, kt + 1, some_waves);
+    if (kt + 2 < kt_end) step(std::integral_constant<int, 2>{}, kt + 2, some_waves);
     }
 
     // Normalise and store: O^T register r of tile j at lane l is hd row
     // 32 j + 8 (r/4) + 4 lg + r%4 of query l%32.
     const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+    if (p.splits > 1) {
+        // A split's partial: O unnormalised, with the max it is relative to
+        // (equal in lanes l and l ^ 32, which exchanged their tile maxima)
+        // and the row sum.
+        if (my_q < S) {
+            const int64_t r = p.cu != nullptr ? row0 + my_q : static_cast<int64_t>(b) * p.S + my_q;
+            const int64_t pr = (static_cast<int64_t>(split) * p.part_rows + r) * p.H + h;
+            if (lg == 0) p.part_ml[pr] = make_float2(m_run, l_tot);
+            float* po = p.part_o + pr * HD;
+#pragma unroll
+            for (int j = 0; j < HT; ++j)
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+                    *reinterpret_cast<float4*>(po + 32 * j + 8 * rb + 4 * lg) =
+                        make_float4(o[j][4 * rb], o[j][4 * rb + 1], o[j][4 * rb + 2],
+                                    o[j][4 * rb + 3]);
+        }
+        return;
+    }
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     if (my_q < S) {
         const int64_t obase =
@@ -708,12 +741,12 @@ void launch_one(const AttnParams& p, hipStream_t stream) {
         // the pipeline choice: the result does not depend on it.
         AttnParams pm = p;
         pm.nqb = (p.S + 127) / 128;
-        const int64_t blocks = static_cast<int64_t>(pm.nqb) * p.B * p.H;
+        const int64_t blocks = static_cast<int64_t>(pm.nqb) * p.B * p.H * p.splits;
         hipLaunchKernelGGL((attn_dma_kernel<HD, 4, 2, OUT_F32, true>),
                            dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, pm);
         return;
     }
-    const int64_t blocks = static_cast<int64_t>(p.nqb) * p.B * p.H;
+    const int64_t blocks = static_cast<int64_t>(p.nqb) * p.B * p.H * p.splits;
     hipLaunchKernelGGL((attn_dma_kernel<HD, NW, NS, OUT_F32, false>),
                        dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0, stream, p);
 }
@@ -763,7 +796,7 @@ void launch_ns(const AttnParams& p, int nw, int ns, hipStream_t stream) {
 // at the default pipeline, else the pipelined one.
 template <int HD>
 bool launch_head_dim(const AttnParams& p, bool out_f32, int nw, int ns, hipStream_t stream) {
-    if (p.S <= 32 && nw == attn_waves_for(p.S) && ns == 0) {
+    if (p.S <= 32 && nw == attn_waves_for(p.S) && ns == 0 && p.splits <= 1) {
         out_f32 ? launch_short<HD, true>(p, stream) : launch_short<HD, false>(p, stream);
         return true;
     }

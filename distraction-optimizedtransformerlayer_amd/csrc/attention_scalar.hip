@@ -34,7 +34,7 @@ __device__ __forceinline__ float widen(T v) {
     return static_cast<float>(v);
 }
 
-template <int HDC, int Q, typename T, bool OUT_F32>
+template <int HDC, int Q, typename T, typename TO>
 __global__ __launch_bounds__(kWaves * 64) void attn_scalar_kernel(AttnParams p, int hd,
                                                                   float scale) {
     __shared__ __attribute__((aligned(16))) float sK[kKT * kKP];
@@ -208,31 +208,30 @@ __global__ __launch_bounds__(kWaves * 64) void attn_scalar_kernel(AttnParams p, 
             const int dd = c * kDC + lane;
             if (dd >= hd) continue;
             const float v = o[qi][c] * inv;
-            if constexpr (OUT_F32) static_cast<float*>(p.out)[obase + dd] = v;
-            else static_cast<_Float16*>(p.out)[obase + dd] = to_half(v);
+            static_cast<TO*>(p.out)[obase + dd] = from_f32<TO>(v);
         }
     }
 }
 
-template <int HDC, int Q, typename T, bool OUT_F32>
+template <int HDC, int Q, typename T, typename TO>
 void launch_q(AttnParams p, int hd, float scale, hipStream_t stream) {
     constexpr int BQ = kWaves * Q;
     p.nqb = (p.S + BQ - 1) / BQ;
     const int64_t blocks = static_cast<int64_t>(p.nqb) * p.B * p.H;
-    hipLaunchKernelGGL((attn_scalar_kernel<HDC, Q, T, OUT_F32>),
+    hipLaunchKernelGGL((attn_scalar_kernel<HDC, Q, T, TO>),
                        dim3(static_cast<unsigned>(blocks)), dim3(kWaves * 64), 0, stream, p, hd,
                        scale);
 }
 
-template <typename T, bool OUT_F32>
+template <typename T, typename TO>
 bool launch_hdc(const AttnParams& p, int hd, float scale, hipStream_t stream) {
     const int hdc = (hd + kDC - 1) / kDC;
-    if (hdc <= 1) launch_q<1, 8, T, OUT_F32>(p, hd, scale, stream);
-    else if (hdc <= 2) launch_q<2, 8, T, OUT_F32>(p, hd, scale, stream);
-    else if (hdc <= 4) launch_q<4, 8, T, OUT_F32>(p, hd, scale, stream);
-    else if (hdc <= 8) launch_q<8, 4, T, OUT_F32>(p, hd, scale, stream);
-    else if (hdc <= 16) launch_q<16, 2, T, OUT_F32>(p, hd, scale, stream);
-    else if (hdc <= 32) launch_q<32, 1, T, OUT_F32>(p, hd, scale, stream);
+    if (hdc <= 1) launch_q<1, 8, T, TO>(p, hd, scale, stream);
+    else if (hdc <= 2) launch_q<2, 8, T, TO>(p, hd, scale, stream);
+    else if (hdc <= 4) launch_q<4, 8, T, TO>(p, hd, scale, stream);
+    else if (hdc <= 8) launch_q<8, 4, T, TO>(p, hd, scale, stream);
+    else if (hdc <= 16) launch_q<16, 2, T, TO>(p, hd, scale, stream);
+    else if (hdc <= 32) launch_q<32, 1, T, TO>(p, hd, scale, stream);
     else return false;
     return true;
 }
@@ -246,15 +245,22 @@ int attn_scalar_query_blocks(int S, int head_dim) {
     return (S + bq - 1) / bq;
 }
 
-bool launch_attn_scalar(const AttnParams& p, int head_dim, bool in_f32, bool out_f32,
+bool launch_attn_scalar(const AttnParams& p, int head_dim, int in_dtype, int out_dtype,
                         float scale, hipStream_t stream) {
     if (head_dim < 1 || head_dim > kMaxScalarHeadDim) return false;
-    if (in_f32) {
-        return out_f32 ? launch_hdc<float, true>(p, head_dim, scale, stream)
-                       : launch_hdc<float, false>(p, head_dim, scale, stream);
+    const bool out32 = out_dtype == DOTL_F32;
+    switch (in_dtype) {
+        case DOTL_F32:
+            return out32 ? launch_hdc<float, float>(p, head_dim, scale, stream)
+                         : launch_hdc<float, _Float16>(p, head_dim, scale, stream);
+        case DOTL_F16:
+            return out32 ? launch_hdc<_Float16, float>(p, head_dim, scale, stream)
+                         : launch_hdc<_Float16, _Float16>(p, head_dim, scale, stream);
+        case DOTL_BF16:
+            return launch_hdc<__bf16, __bf16>(p, head_dim, scale, stream);
+        default:
+            return false;
     }
-    return out_f32 ? launch_hdc<_Float16, true>(p, head_dim, scale, stream)
-                   : launch_hdc<_Float16, false>(p, head_dim, scale, stream);
 }
 
 }  // namespace dotl

@@ -12,6 +12,8 @@ std::atomic<int> g_wmma_fp16{1};
 std::atomic<int> g_cp_async{2};
 std::atomic<int> g_attn_nw{0};
 std::atomic<int> g_attn_ns{0};
+std::atomic<int> g_split_enabled{1};
+std::atomic<int> g_split_forced{0};
 }  // namespace
 
 void set_error(const std::string& msg) { g_last_error = msg; }
@@ -31,6 +33,10 @@ int attention_cp_async_mode() { return g_cp_async.load(std::memory_order_relaxed
 void attention_pipeline(int* nw, int* ns) {
     *nw = g_attn_nw.load(std::memory_order_relaxed);
     *ns = g_attn_ns.load(std::memory_order_relaxed);
+}
+void attention_split_knobs(int* enabled, int* forced) {
+    *enabled = g_split_enabled.load(std::memory_order_relaxed);
+    *forced = g_split_forced.load(std::memory_order_relaxed);
 }
 
 namespace {
@@ -150,5 +156,8 @@ void dotl_attention_set_pipeline(int waves, int stages) {
     dotl::g_attn_ns.store(stages);
 }
 int dotl_wmma_cp_async_mode(void) { return dotl::g_cp_async.load(); }
+void dotl_wmma_set_split_kv(int on) { dotl::g_split_enabled.store(on ? 1 : 0); }
+int dotl_wmma_split_kv_enabled(void) { return dotl::g_split_enabled.load(); }
+void dotl_wmma_set_split_count(int n) { dotl::g_split_forced.store(n > 0 ? n : 0); }
 
 }  // extern "C"

@@ -23,6 +23,51 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// ---- tensor element types --------------------------------------------------
+// float, _Float16 and __bf16 are the tensor dtypes DOTL_F32 / DOTL_F16 /
+// DOTL_BF16. Conversions to 16-bit types round to nearest even (the hardware
+// v_cvt_f16_f32 / v_cvt_pk_bf16_f32).
+
+template <typename T> struct dtype_code;
+template <> struct dtype_code<float> { static constexpr int value = DOTL_F32; };
+template <> struct dtype_code<_Float16> { static constexpr int value = DOTL_F16; };
+template <> struct dtype_code<__bf16> { static constexpr int value = DOTL_BF16; };
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v) { return static_cast<T>(v); }
+
+// v rounded through T and back (the identity for float).
+template <typename T>
+__device__ __forceinline__ float round_via(float v) { return static_cast<float>(static_cast<T>(v)); }
+
+// Four consecutive elements as a float4; p is aligned to 4 * sizeof(T).
+template <typename T>
+__device__ __forceinline__ float4 load4f(const T* p) {
+    if constexpr (sizeof(T) == 4) {
+        return *reinterpret_cast<const float4*>(p);
+    } else {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        const t4 h = *reinterpret_cast<const t4*>(p);
+        return make_float4(static_cast<float>(h[0]), static_cast<float>(h[1]),
+                           static_cast<float>(h[2]), static_cast<float>(h[3]));
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void store4f(T* p, float4 v) {
+    if constexpr (sizeof(T) == 4) {
+        *reinterpret_cast<float4*>(p) = v;
+    } else {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        t4 h;
+        h[0] = static_cast<T>(v.x); h[1] = static_cast<T>(v.y);
+        h[2] = static_cast<T>(v.z); h[3] = static_cast<T>(v.w);
+        *reinterpret_cast<t4*>(p) = h;
+    }
+}
 
 // ---- error channel ---------------------------------------------------------
 

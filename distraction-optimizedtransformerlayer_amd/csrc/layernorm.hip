@@ -35,62 +35,100 @@ namespace {
 
 constexpr int kRowsPerBlock = 4;
 
-__device__ __forceinline__ int64_t D_of(int nchunk) { return 4 * static_cast<int64_t>(nchunk); }
+// Storage type of each normed-output code.
+template <int NORMED> struct normed_type { using type = float; };
+template <> struct normed_type<DOTL_F16> { using type = _Float16; };
+template <> struct normed_type<DOTL_F16X2> { using type = _Float16; };
+template <> struct normed_type<DOTL_BF16> { using type = __bf16; };
 
-template <bool HAS_SUB>
-__device__ __forceinline__ float4 load_sum4(const float* __restrict__ x,
-                                            const float* __restrict__ sub, int64_t off) {
-    float4 a = *reinterpret_cast<const float4*>(x + off);
+// Graph I/O slot (optional): io[0] replaces the x pointer when bit 0 of
+// io_mode is set, io[1] the normed pointer when bit 1 is. A captured graph
+// bakes in the slot's address, not the tensors', so each replay reads the
+// caller's input and writes the caller's output where the slot points.
+#define DOTL_LN_RESOLVE_IO()                                                \
+    do {                                                                    \
+        if (io_mode & 1) x = reinterpret_cast<const TI*>(io[0]);            \
+        if (io_mode & 2) normed = reinterpret_cast<void*>(io[1]);           \
+    } while (0)
+
+// x (+ sub), as the tensor dtype holds the sum: x_new = TI(x + sub).
+template <typename TI, bool HAS_SUB>
+__device__ __forceinline__ float4 load_sum4(const TI* __restrict__ x, const TI* __restrict__ sub,
+                                            int64_t off) {
+    float4 a = load4f(x + off);
     if constexpr (HAS_SUB) {
-        const float4 s = *reinterpret_cast<const float4*>(sub + off);
-        a.x += s.x; a.y += s.y; a.z += s.z; a.w += s.w;
+        const float4 s = load4f(sub + off);
+        a.x = round_via<TI>(a.x + s.x); a.y = round_via<TI>(a.y + s.y);
+        a.z = round_via<TI>(a.z + s.z); a.w = round_via<TI>(a.w + s.w);
     }
     return a;
 }
 
-// A row whose index entry is negative: every output of the row is zero.
-template <int CH, bool WRITE_XNEW, int NORMED>
-__device__ __forceinline__ void zero_row_vec(float* __restrict__ x_new, void* __restrict__ normed,
-                                             int64_t rows, int64_t base, int nchunk, int lane) {
-    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const int idx = c * 64 + lane;
-        if (idx < nchunk) {
-            const int col = 4 * idx;
-            if constexpr (WRITE_XNEW) *reinterpret_cast<float4*>(x_new + base + col) = z;
-            if constexpr (NORMED == DOTL_F16 || NORMED == DOTL_F16X2) {
-                const half4 hz = {};
-                *reinterpret_cast<half4*>(static_cast<_Float16*>(normed) + base + col) = hz;
-                if constexpr (NORMED == DOTL_F16X2)
-                    *reinterpret_cast<half4*>(static_cast<_Float16*>(normed) + rows * D_of(nchunk) + base + col) = hz;
-            } else {
-                *reinterpret_cast<float4*>(static_cast<float*>(normed) + base + col) = z;
-            }
-        }
+// Four normalised values to the normed output (split planes: hi, then lo
+// in the second [rows, D] plane).
+template <int NORMED>
+__device__ __forceinline__ void store_normed4(void* __restrict__ normed, int64_t plane,
+                                             int64_t off, float4 o) {
+    using TO = typename normed_type<NORMED>::type;
+    TO* out = static_cast<TO*>(normed);
+    if constexpr (NORMED == DOTL_F16X2) {
+        half4 h, l;
+        h[0] = to_half(o.x); h[1] = to_half(o.y); h[2] = to_half(o.z); h[3] = to_half(o.w);
+        l[0] = split_lo(o.x, h[0]); l[1] = split_lo(o.y, h[1]);
+        l[2] = split_lo(o.z, h[2]); l[3] = split_lo(o.w, h[3]);
+        *reinterpret_cast<half4*>(out + off) = h;
+        *reinterpret_cast<half4*>(out + plane + off) = l;
+    } else {
+        store4f(out + off, o);
+    }
+}
+
+template <int NORMED>
+__device__ __forceinline__ void store_normed1(void* __restrict__ normed, int64_t plane,
+                                              int64_t off, float o) {
+    using TO = typename normed_type<NORMED>::type;
+    TO* out = static_cast<TO*>(normed);
+    if constexpr (NORMED == DOTL_F16X2) {
+        const _Float16 h = to_half(o);
+        out[off] = h;
+        out[plane + off] = split_lo(o, h);
+    } else {
+        out[off] = from_f32<TO>(o);
     }
 }
 
 // Vector path: D % 4 == 0 and D <= 256 * CH. Chunk c of lane l covers row
-// elements [4 * (c * 64 + l), +4).
-template <int CH, bool HAS_SUB, bool WRITE_XNEW, int NORMED>
+// elements [4 * (c * 64 + l), +4): 16-byte accesses for fp32, 8-byte for
+// the 16-bit types.
+template <typename TI, int CH, bool HAS_SUB, bool WRITE_XNEW, int NORMED>
 __global__ __launch_bounds__(256) void layernorm_vec_kernel(
-    const float* __restrict__ x, const float* __restrict__ sub,
-    const float* __restrict__ w, const float* __restrict__ b,
-    float* __restrict__ x_new, void* __restrict__ normed,
-    const int32_t* __restrict__ row_index, int64_t in_rows, int64_t rows, int D, float eps) {
+    const TI* __restrict__ x, const TI* __restrict__ sub,
+    const TI* __restrict__ w, const TI* __restrict__ b,
+    TI* __restrict__ x_new, void* __restrict__ normed,
+    const int32_t* __restrict__ row_index, int64_t in_rows, int64_t rows, int D, float eps,
+    const int64_t* __restrict__ io, int io_mode) {
+    DOTL_LN_RESOLVE_IO();
     const int lane = threadIdx.x & 63;
     const int64_t wave_global = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
     const int64_t wave_stride = static_cast<int64_t>(gridDim.x) * kRowsPerBlock;
     const int nchunk = D >> 2;
     const float inv_d = 1.0f / static_cast<float>(D);
+    const int64_t plane = rows * D;
 
     for (int64_t row = wave_global; row < rows; row += wave_stride) {
         const int64_t base = row * D;   // output row
         int64_t src = row_index ? static_cast<int64_t>(row_index[row]) : row;
         if (src >= in_rows) src = -1;
         if (src < 0) {
-            zero_row_vec<CH, WRITE_XNEW, NORMED>(x_new, normed, rows, base, nchunk, lane);
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int idx = c * 64 + lane;
+                if (idx < nchunk) {
+                    if constexpr (WRITE_XNEW) store4f(x_new + base + 4 * idx, z);
+                    store_normed4<NORMED>(normed, plane, base + 4 * idx, z);
+                }
+            }
             continue;
         }
         const int64_t ibase = src * D;  // input row
@@ -100,7 +138,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
         for (int c = 0; c < CH; ++c) {
             const int idx = c * 64 + lane;
             if (idx < nchunk) {
-                v[c] = load_sum4<HAS_SUB>(x, sub, ibase + 4 * idx);
+                v[c] = load_sum4<TI, HAS_SUB>(x, sub, ibase + 4 * idx);
             } else {
                 v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
@@ -135,47 +173,36 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
             const int idx = c * 64 + lane;
             if (idx < nchunk) {
                 const int col = 4 * idx;
-                if constexpr (WRITE_XNEW) {
-                    *reinterpret_cast<float4*>(x_new + base + col) = v[c];
-                }
-                const float4 ww = *reinterpret_cast<const float4*>(w + col);
-                const float4 bb = *reinterpret_cast<const float4*>(b + col);
+                if constexpr (WRITE_XNEW) store4f(x_new + base + col, v[c]);
+                const float4 ww = load4f(w + col);
+                const float4 bb = load4f(b + col);
                 float4 o;
                 o.x = ln_out(v[c].x, mean_est, delta, rstd, ww.x, bb.x);
                 o.y = ln_out(v[c].y, mean_est, delta, rstd, ww.y, bb.y);
                 o.z = ln_out(v[c].z, mean_est, delta, rstd, ww.z, bb.z);
                 o.w = ln_out(v[c].w, mean_est, delta, rstd, ww.w, bb.w);
-                if constexpr (NORMED == DOTL_F16 || NORMED == DOTL_F16X2) {
-                    half4 h;
-                    h[0] = to_half(o.x); h[1] = to_half(o.y);
-                    h[2] = to_half(o.z); h[3] = to_half(o.w);
-                    *reinterpret_cast<half4*>(static_cast<_Float16*>(normed) + base + col) = h;
-                    if constexpr (NORMED == DOTL_F16X2) {
-                        half4 l;
-                        l[0] = split_lo(o.x, h[0]); l[1] = split_lo(o.y, h[1]);
-                        l[2] = split_lo(o.z, h[2]); l[3] = split_lo(o.w, h[3]);
-                        *reinterpret_cast<half4*>(static_cast<_Float16*>(normed) + rows * D + base + col) = l;
-                    }
-                } else {
-                    *reinterpret_cast<float4*>(static_cast<float*>(normed) + base + col) = o;
-                }
+                store_normed4<NORMED>(normed, plane, base + col, o);
             }
         }
     }
 }
 
 // Scalar path for any D in [1, 64 * EPL]: element e of lane l is column
-// e * 64 + l. Used when D % 4 != 0 (the vector path's 16-byte accesses need it).
-template <int EPL, bool HAS_SUB, bool WRITE_XNEW, int NORMED>
+// e * 64 + l. Used when D % 4 != 0 or a tensor is not aligned for the
+// vector accesses.
+template <typename TI, int EPL, bool HAS_SUB, bool WRITE_XNEW, int NORMED>
 __global__ __launch_bounds__(256) void layernorm_scalar_kernel(
-    const float* __restrict__ x, const float* __restrict__ sub,
-    const float* __restrict__ w, const float* __restrict__ b,
-    float* __restrict__ x_new, void* __restrict__ normed,
-    const int32_t* __restrict__ row_index, int64_t in_rows, int64_t rows, int D, float eps) {
+    const TI* __restrict__ x, const TI* __restrict__ sub,
+    const TI* __restrict__ w, const TI* __restrict__ b,
+    TI* __restrict__ x_new, void* __restrict__ normed,
+    const int32_t* __restrict__ row_index, int64_t in_rows, int64_t rows, int D, float eps,
+    const int64_t* __restrict__ io, int io_mode) {
+    DOTL_LN_RESOLVE_IO();
     const int lane = threadIdx.x & 63;
     const int64_t wave_global = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
     const int64_t wave_stride = static_cast<int64_t>(gridDim.x) * kRowsPerBlock;
     const float inv_d = 1.0f / static_cast<float>(D);
+    const int64_t plane = rows * D;
 
     for (int64_t row = wave_global; row < rows; row += wave_stride) {
         const int64_t base = row * D;   // output row
@@ -186,14 +213,8 @@ __global__ __launch_bounds__(256) void layernorm_scalar_kernel(
             for (int e = 0; e < EPL; ++e) {
                 const int col = e * 64 + lane;
                 if (col < D) {
-                    if constexpr (WRITE_XNEW) x_new[base + col] = 0.f;
-                    if constexpr (NORMED == DOTL_F16 || NORMED == DOTL_F16X2) {
-                        static_cast<_Float16*>(normed)[base + col] = static_cast<_Float16>(0.f);
-                        if constexpr (NORMED == DOTL_F16X2)
-                            static_cast<_Float16*>(normed)[rows * D + base + col] = static_cast<_Float16>(0.f);
-                    } else {
-                        static_cast<float*>(normed)[base + col] = 0.f;
-                    }
+                    if constexpr (WRITE_XNEW) x_new[base + col] = from_f32<TI>(0.f);
+                    store_normed1<NORMED>(normed, plane, base + col, 0.f);
                 }
             }
             continue;
@@ -206,8 +227,8 @@ __global__ __launch_bounds__(256) void layernorm_scalar_kernel(
             const int col = e * 64 + lane;
             float a = 0.f;
             if (col < D) {
-                a = x[ibase + col];
-                if constexpr (HAS_SUB) a += sub[ibase + col];
+                a = static_cast<float>(x[ibase + col]);
+                if constexpr (HAS_SUB) a = round_via<TI>(a + static_cast<float>(sub[ibase + col]));
             }
             v[e] = a;
             s += a;
@@ -234,33 +255,29 @@ __global__ __launch_bounds__(256) void layernorm_scalar_kernel(
         for (int e = 0; e < EPL; ++e) {
             const int col = e * 64 + lane;
             if (col < D) {
-                if constexpr (WRITE_XNEW) x_new[base + col] = v[e];
-                const float o = ln_out(v[e], mean_est, delta, rstd, w[col], b[col]);
-                if constexpr (NORMED == DOTL_F16 || NORMED == DOTL_F16X2) {
-                    const _Float16 h = to_half(o);
-                    static_cast<_Float16*>(normed)[base + col] = h;
-                    if constexpr (NORMED == DOTL_F16X2)
-                        static_cast<_Float16*>(normed)[rows * D + base + col] = split_lo(o, h);
-                } else {
-                    static_cast<float*>(normed)[base + col] = o;
-                }
+                if constexpr (WRITE_XNEW) x_new[base + col] = from_f32<TI>(v[e]);
+                const float o = ln_out(v[e], mean_est, delta, rstd, static_cast<float>(w[col]),
+                                       static_cast<float>(b[col]));
+                store_normed1<NORMED>(normed, plane, base + col, o);
             }
         }
     }
 }
 
 struct LnArgs {
-    const float* x;
-    const float* sub;
-    const float* w;
-    const float* b;
-    float* x_new;
+    const void* x;
+    const void* sub;
+    const void* w;
+    const void* b;
+    void* x_new;
     void* normed;
     const int32_t* row_index;
     int64_t in_rows;
     int64_t rows;
     int D;
     float eps;
+    const int64_t* io;
+    int io_mode;
     hipStream_t stream;
 };
 
@@ -272,88 +289,130 @@ unsigned grid_for(int64_t rows) {
     return static_cast<unsigned>(want < cap ? (want > 0 ? want : 1) : cap);
 }
 
-template <int CH, bool HAS_SUB, bool WX, int F16>
+template <typename TI, int CH, bool HAS_SUB, bool WX, int NO>
 void launch_vec(const LnArgs& a) {
-    hipLaunchKernelGGL((layernorm_vec_kernel<CH, HAS_SUB, WX, F16>), dim3(grid_for(a.rows)),
-                       dim3(256), 0, a.stream, a.x, a.sub, a.w, a.b, a.x_new, a.normed,
-                       a.row_index, a.in_rows, a.rows, a.D, a.eps);
+    hipLaunchKernelGGL((layernorm_vec_kernel<TI, CH, HAS_SUB, WX, NO>), dim3(grid_for(a.rows)),
+                       dim3(256), 0, a.stream, static_cast<const TI*>(a.x),
+                       static_cast<const TI*>(a.sub), static_cast<const TI*>(a.w),
+                       static_cast<const TI*>(a.b), static_cast<TI*>(a.x_new), a.normed,
+                       a.row_index, a.in_rows, a.rows, a.D, a.eps, a.io, a.io_mode);
 }
 
-template <int EPL, bool HAS_SUB, bool WX, int F16>
+template <typename TI, int EPL, bool HAS_SUB, bool WX, int NO>
 void launch_scalar(const LnArgs& a) {
-    hipLaunchKernelGGL((layernorm_scalar_kernel<EPL, HAS_SUB, WX, F16>), dim3(grid_for(a.rows)),
-                       dim3(256), 0, a.stream, a.x, a.sub, a.w, a.b, a.x_new, a.normed,
-                       a.row_index, a.in_rows, a.rows, a.D, a.eps);
+    hipLaunchKernelGGL((layernorm_scalar_kernel<TI, EPL, HAS_SUB, WX, NO>), dim3(grid_for(a.rows)),
+                       dim3(256), 0, a.stream, static_cast<const TI*>(a.x),
+                       static_cast<const TI*>(a.sub), static_cast<const TI*>(a.w),
+                       static_cast<const TI*>(a.b), static_cast<TI*>(a.x_new), a.normed,
+                       a.row_index, a.in_rows, a.rows, a.D, a.eps, a.io, a.io_mode);
 }
 
-template <bool HAS_SUB, bool WX, int F16>
+template <typename TI, bool HAS_SUB, bool WX, int NO>
 void dispatch_width(const LnArgs& a, bool vec) {
     const int D = a.D;
     if (vec) {
-        if (D <= 256) launch_vec<1, HAS_SUB, WX, F16>(a);
-        else if (D <= 512) launch_vec<2, HAS_SUB, WX, F16>(a);
-        else if (D <= 1024) launch_vec<4, HAS_SUB, WX, F16>(a);
-        else if (D <= 2048) launch_vec<8, HAS_SUB, WX, F16>(a);
-        else if (D <= 4096) launch_vec<16, HAS_SUB, WX, F16>(a);
-        else launch_vec<32, HAS_SUB, WX, F16>(a);
+        if (D <= 256) launch_vec<TI, 1, HAS_SUB, WX, NO>(a);
+        else if (D <= 512) launch_vec<TI, 2, HAS_SUB, WX, NO>(a);
+        else if (D <= 1024) launch_vec<TI, 4, HAS_SUB, WX, NO>(a);
+        else if (D <= 2048) launch_vec<TI, 8, HAS_SUB, WX, NO>(a);
+        else if (D <= 4096) launch_vec<TI, 16, HAS_SUB, WX, NO>(a);
+        else launch_vec<TI, 32, HAS_SUB, WX, NO>(a);
     } else {
-        if (D <= 64) launch_scalar<1, HAS_SUB, WX, F16>(a);
-        else if (D <= 256) launch_scalar<4, HAS_SUB, WX, F16>(a);
-        else if (D <= 1024) launch_scalar<16, HAS_SUB, WX, F16>(a);
-        else if (D <= 4096) launch_scalar<64, HAS_SUB, WX, F16>(a);
-        else launch_scalar<128, HAS_SUB, WX, F16>(a);
+        if (D <= 64) launch_scalar<TI, 1, HAS_SUB, WX, NO>(a);
+        else if (D <= 256) launch_scalar<TI, 4, HAS_SUB, WX, NO>(a);
+        else if (D <= 1024) launch_scalar<TI, 16, HAS_SUB, WX, NO>(a);
+        else if (D <= 4096) launch_scalar<TI, 64, HAS_SUB, WX, NO>(a);
+        else launch_scalar<TI, 128, HAS_SUB, WX, NO>(a);
+    }
+}
+
+template <typename TI, int NO>
+void dispatch_flags(const LnArgs& a, bool vec) {
+    if (a.sub) {
+        if (a.x_new) dispatch_width<TI, true, true, NO>(a, vec);
+        else dispatch_width<TI, true, false, NO>(a, vec);
+    } else {
+        if (a.x_new) dispatch_width<TI, false, true, NO>(a, vec);
+        else dispatch_width<TI, false, false, NO>(a, vec);
     }
 }
 
 }  // namespace
 }  // namespace dotl
 
-extern "C" int dotl_layernorm(const void* x, const void* sub, const float* weight,
-                              const float* bias, void* x_new, void* normed,
+extern "C" int dotl_layernorm(const void* x, const void* sub, const void* weight,
+                              const void* bias, void* x_new, void* normed,
                               const int32_t* row_index, int64_t in_rows, int64_t rows,
                               int64_t D, double eps, int dtype, int normed_dtype,
-                              void* stream) {
+                              const int64_t* io, int io_mode, void* stream) {
     using namespace dotl;
     clear_error();
     const char* who = sub ? "fused_add_layernorm" : "fused_layernorm";
-    if (dtype != DOTL_F32) {
-        set_error(std::string(who) + ": this build serves float32 tensors only");
-        return DOTL_DECLINED;
+    DOTL_REQUIRE(dtype == DOTL_F32 || dtype == DOTL_F16 || dtype == DOTL_BF16,
+                 "%s: x must be float32, float16 or bfloat16", who);
+    if (dtype == DOTL_F32) {
+        DOTL_REQUIRE(normed_dtype == DOTL_F32 || normed_dtype == DOTL_F16 ||
+                         normed_dtype == DOTL_F16X2,
+                     "%s: the normed output of a float32 x is float32, float16 or split float16",
+                     who);
+    } else {
+        DOTL_REQUIRE(normed_dtype == dtype, "%s: the normed output of a %s x has x's dtype", who,
+                     dtype == DOTL_F16 ? "float16" : "bfloat16");
     }
-    DOTL_REQUIRE(normed_dtype == DOTL_F32 || normed_dtype == DOTL_F16 || normed_dtype == DOTL_F16X2,
-                 "%s: normed dtype must be float32, float16 or split float16", who);
     DOTL_REQUIRE(D >= 1 && D <= 8192, "%s: last dimension %lld outside [1, 8192]", who,
                  static_cast<long long>(D));
     DOTL_REQUIRE(rows >= 0, "%s: negative row count", who);
     DOTL_REQUIRE(row_index == nullptr || in_rows >= 0, "%s: negative input row count", who);
+    DOTL_REQUIRE(io_mode >= 0 && io_mode <= 3, "%s: io_mode must be in [0, 3]", who);
+    DOTL_REQUIRE(io_mode == 0 || io != nullptr, "%s: io_mode %d needs an io slot", who, io_mode);
     if (rows == 0) return DOTL_OK;
-    DOTL_REQUIRE(x && weight && bias && normed, "%s: null pointer", who);
+    DOTL_REQUIRE((x || (io_mode & 1)) && weight && bias && (normed || (io_mode & 2)),
+                 "%s: null pointer", who);
 
-    const bool aligned =
-        (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(sub) |
-         reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias) |
-         reinterpret_cast<uintptr_t>(x_new) | reinterpret_cast<uintptr_t>(normed)) % 16 == 0;
-    const bool vec = (D % 4 == 0) && aligned;
+    // Slot-addressed tensors are not known here; the caller guarantees they
+    // are allocations of the shapes given (16-byte aligned, as torch's are).
+    const size_t esize = dtype == DOTL_F32 ? 4 : 2;
+    const uintptr_t addr_or =
+        reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(sub) |
+        reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias) |
+        reinterpret_cast<uintptr_t>(x_new) | reinterpret_cast<uintptr_t>(normed);
+    const bool vec = (D % 4 == 0) && addr_or % (4 * esize) == 0 && (io_mode == 0 || D % 4 == 0);
 
-    LnArgs a{static_cast<const float*>(x), static_cast<const float*>(sub), weight, bias,
-             static_cast<float*>(x_new), normed, row_index, row_index ? in_rows : rows, rows,
-             static_cast<int>(D),
-             static_cast<float>(eps), as_stream(stream)};
-    auto by_out = [&](auto has_sub, auto wx) {
-        constexpr bool HS = decltype(has_sub)::value;
-        constexpr bool WX = decltype(wx)::value;
-        switch (normed_dtype) {
-            case DOTL_F16: dispatch_width<HS, WX, DOTL_F16>(a, vec); break;
-            case DOTL_F16X2: dispatch_width<HS, WX, DOTL_F16X2>(a, vec); break;
-            default: dispatch_width<HS, WX, DOTL_F32>(a, vec); break;
-        }
-    };
-    if (sub) {
-        if (x_new) by_out(std::true_type{}, std::true_type{});
-        else by_out(std::true_type{}, std::false_type{});
-    } else {
-        if (x_new) by_out(std::false_type{}, std::true_type{});
-        else by_out(std::false_type{}, std::false_type{});
+    LnArgs a{x, sub, weight, bias, x_new, normed, row_index, row_index ? in_rows : rows, rows,
+             static_cast<int>(D), static_cast<float>(eps), io, io_mode, as_stream(stream)};
+    switch (dtype) {
+        case DOTL_F16: dispatch_flags<_Float16, DOTL_F16>(a, vec); break;
+        case DOTL_BF16: dispatch_flags<__bf16, DOTL_BF16>(a, vec); break;
+        default:
+            switch (normed_dtype) {
+                case DOTL_F16: dispatch_flags<float, DOTL_F16>(a, vec); break;
+                case DOTL_F16X2: dispatch_flags<float, DOTL_F16X2>(a, vec); break;
+                default: dispatch_flags<float, DOTL_F32>(a, vec); break;
+            }
+            break;
     }
     return check_launch(who);
+}
+
+// Writes two addresses into a graph I/O slot, in stream order: the launch
+// that rebinds a captured graph's input and output before each replay.
+namespace dotl {
+namespace {
+__global__ void bind_io_kernel(int64_t* __restrict__ slot, int64_t a, int64_t b) {
+    if (threadIdx.x == 0) {
+        slot[0] = a;
+        slot[1] = b;
+    }
+}
+}  // namespace
+}  // namespace dotl
+
+extern "C" int dotl_bind_io(int64_t* slot, const void* in, void* out, void* stream) {
+    using namespace dotl;
+    clear_error();
+    DOTL_REQUIRE(slot != nullptr, "bind_io: null slot");
+    hipLaunchKernelGGL(bind_io_kernel, dim3(1), dim3(64), 0, as_stream(stream), slot,
+                       static_cast<int64_t>(reinterpret_cast<uintptr_t>(in)),
+                       static_cast<int64_t>(reinterpret_cast<uintptr_t>(out)));
+    return check_launch("bind_io");
 }

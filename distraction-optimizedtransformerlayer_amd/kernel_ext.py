@@ -37,13 +37,14 @@ _THIS_DIR = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_THIS_DIR, "libdotl_hip.so")
 _CSRC = os.path.join(_THIS_DIR, "csrc")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DOTL_OK = 0
 DOTL_DECLINED = 1
 DOTL_F32 = 0
 DOTL_F16 = 1
 DOTL_F16X2 = 2
+DOTL_BF16 = 3
 DOTL_ACT_NONE = 0
 DOTL_ACT_GELU = 1
 DOTL_MATH_FP16 = 0
@@ -56,7 +57,9 @@ EXPORTED_SYMBOLS = (
     "dotl_mfma_layout_probe", "dotl_layernorm", "dotl_weight_split", "dotl_linear",
     "dotl_attention_forward", "dotl_ffn_block", "dotl_wmma_set_fp16", "dotl_wmma_fp16",
     "dotl_wmma_set_cp_async", "dotl_wmma_cp_async_mode", "dotl_lds_dma_probe",
-    "dotl_attention_set_pipeline", "dotl_linear_residual",
+    "dotl_attention_set_pipeline", "dotl_linear_residual", "dotl_bind_io",
+    "dotl_attention_split_plan", "dotl_wmma_set_split_kv", "dotl_wmma_split_kv_enabled",
+    "dotl_wmma_set_split_count",
 )
 
 _kernels = None
@@ -102,7 +105,9 @@ def _declare(lib) -> None:
     lib.dotl_lds_dma_probe.argtypes = [vp, vp, vp]
     lib.dotl_layernorm.restype = i32
     lib.dotl_layernorm.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, c.c_double, i32,
-                                   i32, vp]
+                                   i32, vp, i32, vp]
+    lib.dotl_bind_io.restype = i32
+    lib.dotl_bind_io.argtypes = [vp, vp, vp, vp]
     lib.dotl_weight_split.restype = i32
     lib.dotl_weight_split.argtypes = [vp, vp, vp, i64, vp]
     lib.dotl_linear.restype = i32
@@ -113,7 +118,15 @@ def _declare(lib) -> None:
     lib.dotl_attention_forward.restype = i32
     lib.dotl_attention_forward.argtypes = [vp, vp, vp, i32, c.POINTER(i64), vp, c.POINTER(i64),
                                            vp, i32, i32, i32, i32, i32, i32, i32, c.c_double,
-                                           i32, i32, vp, vp]
+                                           i32, i32, vp, i64, i32, vp, i64, vp]
+    lib.dotl_attention_split_plan.restype = i32
+    lib.dotl_attention_split_plan.argtypes = [i32, i32, i32, i32, i32, i32, i32, i64, i32, i32,
+                                              i32, c.POINTER(i32), c.POINTER(i64)]
+    lib.dotl_wmma_set_split_kv.restype = None
+    lib.dotl_wmma_set_split_kv.argtypes = [i32]
+    lib.dotl_wmma_split_kv_enabled.restype = i32
+    lib.dotl_wmma_set_split_count.restype = None
+    lib.dotl_wmma_set_split_count.argtypes = [i32]
     lib.dotl_ffn_block.restype = i32
     lib.dotl_ffn_block.argtypes = [vp] * 12 + [i64, i64, i64, c.c_double, vp]
     lib.dotl_wmma_set_fp16.restype = None
@@ -152,6 +165,8 @@ def _dtype_code(t) -> Optional[int]:
         return DOTL_F32
     if t.dtype == torch.float16:
         return DOTL_F16
+    if t.dtype == torch.bfloat16:
+        return DOTL_BF16
     return None
 
 
@@ -161,12 +176,12 @@ class Kernels:
     def __init__(self, lib) -> None:
         self._lib = lib
         self._wcache: Dict[int, Tuple[weakref.ReferenceType, tuple, object, object]] = {}
+        self._wcache_builds = 0
         self._tile_split_kv = False
         self._layernorm_knobs = {"block_threads": 0, "warp_width": -1, "warp_rows": 0,
                                  "fused_reduce": True}
         self._wmma_flags = {"softmax_mode": 1, "mask_classify": True, "acc_formula": True,
-                            "direct_o": True, "split_kv": True, "split_count": 0,
-                            "causal_reverse": True}
+                            "direct_o": True, "causal_reverse": True}
 
     # -- plumbing ----------------------------------------------------------------
 
@@ -228,13 +243,22 @@ class Kernels:
     # -- LayerNorm (reference csrc/add_layernorm.cuh:491-692) -----------------------
 
     def _layernorm(self, who, x, sub, weight, bias, eps, normed_half, write_xnew=True,
-                   split=False, row_index=None):
+                   split=False, row_index=None, io=None, copy_x=False):
         """Shared body of the LayerNorm methods.
 
         x_new is written when `write_xnew` and either a residual is added or a
         row index is given (then it is the gathered x). With `row_index`
         (int32 [rows], device), x/sub are read as [in_rows, D] and both
         outputs are [rows, D]; an entry outside [0, in_rows) gives zero rows.
+        x may be float32, float16 or bfloat16 (weight and bias in the same
+        dtype); x_new and the normed output then have x's dtype, except that
+        a float32 x may ask for an fp16 (`normed_half`) or split (`split`)
+        normed output.
+
+        `io` = (slot, mode) binds the kernel's x (mode bit 0) and/or normed
+        (bit 1) pointer to the device int64 [2] `slot` (a graph I/O slot,
+        see bind_io): the kernel then reads/writes there instead of x /
+        the normed tensor returned here, which only stands in for its shape.
         """
         import torch
 
@@ -252,10 +276,11 @@ class Kernels:
                                    f"{tuple(x.shape)} and {tuple(sub.shape)}")
             if sub.dtype != x.dtype:
                 raise RuntimeError(f"{who}: x and sub must share a dtype")
-        if normed_half and x.dtype != torch.float32:
+        if (normed_half or split) and x.dtype != torch.float32:
             raise RuntimeError(f"{who}: normed_half is only defined for an fp32 input, got {x.dtype}")
-        if x.dtype != torch.float32:
-            raise RuntimeError(f"{who}: this build serves float32 tensors only, got {x.dtype}")
+        xcode = _dtype_code(x)
+        if xcode is None:
+            raise RuntimeError(f"{who}: x must be float32, float16 or bfloat16, got {x.dtype}")
         xc = x.contiguous()
         sc = sub.contiguous() if sub is not None else None
         wc, bc = weight.contiguous(), bias.contiguous()
@@ -270,27 +295,48 @@ class Kernels:
             ri = None
             rows = in_rows
             out_shape = tuple(xc.shape)
-        want_xnew = write_xnew and (sc is not None or ri is not None)
+        want_xnew = (write_xnew and (sc is not None or ri is not None)) or copy_x
         x_new = torch.empty(out_shape, dtype=xc.dtype, device=xc.device) if want_xnew else None
         if split:
             normed = torch.empty((2, *out_shape), dtype=torch.float16, device=xc.device)
             ncode = DOTL_F16X2
+        elif normed_half:
+            normed = torch.empty(out_shape, dtype=torch.float16, device=xc.device)
+            ncode = DOTL_F16
         else:
-            normed = torch.empty(out_shape, dtype=torch.float16 if normed_half else torch.float32,
-                                 device=xc.device)
-            ncode = DOTL_F16 if normed_half else DOTL_F32
+            normed = torch.empty(out_shape, dtype=xc.dtype, device=xc.device)
+            ncode = xcode
+        slot_ptr, mode = None, 0
+        if io is not None:
+            slot, mode = io
+            if slot.dtype != torch.int64 or slot.numel() < 2 or not slot.is_cuda:
+                raise RuntimeError(f"{who}: the io slot must be a CUDA int64 tensor of 2")
+            slot_ptr = slot.data_ptr()
         rc = self._lib.dotl_layernorm(
             xc.data_ptr(), sc.data_ptr() if sc is not None else None, wc.data_ptr(),
             bc.data_ptr(), x_new.data_ptr() if x_new is not None else None, normed.data_ptr(),
-            ri.data_ptr() if ri is not None else None, in_rows, rows, D, float(eps), DOTL_F32,
-            ncode, self._stream(x.device))
+            ri.data_ptr() if ri is not None else None, in_rows, rows, D, float(eps), xcode,
+            ncode, slot_ptr, int(mode), self._stream(x.device))
         self._check(rc)
         if rc == DOTL_DECLINED:
             raise RuntimeError(self._err())
         return x_new, normed
 
+    def bind_io(self, slot, src, dst) -> None:
+        """slot[0] = src's address, slot[1] = dst's (either may be None: 0),
+        written in stream order on the current stream: rebinds the kernels
+        of a captured graph that read/write through `slot` (the `io`
+        argument of the LayerNorm methods). Not in the reference's surface."""
+        import torch
+
+        if slot.dtype != torch.int64 or slot.numel() < 2 or not slot.is_cuda:
+            raise RuntimeError("bind_io: the slot must be a CUDA int64 tensor of 2")
+        self._check(self._lib.dotl_bind_io(
+            slot.data_ptr(), src.data_ptr() if src is not None else None,
+            dst.data_ptr() if dst is not None else None, self._stream(slot.device)))
+
     def fused_layernorm_rows(self, x, weight, bias, row_index, eps=1e-5, normed="float",
-                             copy_x=True):
+                             copy_x=True, io=None):
         """[x[row_index], LayerNorm(x[row_index])]: the gather into packed rows.
 
         Not in the reference's surface. `x` is [..., D] read as [in_rows, D];
@@ -300,10 +346,10 @@ class Kernels:
         """
         x_rows, out = self._layernorm("fused_layernorm", x, None, weight, bias, eps,
                                       normed == "half", write_xnew=copy_x,
-                                      split=normed == "split", row_index=row_index)
+                                      split=normed == "split", row_index=row_index, io=io)
         return [x_rows, out]
 
-    def fused_add_layernorm_rows(self, x, sub, weight, bias, row_index, eps=1e-5):
+    def fused_add_layernorm_rows(self, x, sub, weight, bias, row_index, eps=1e-5, io=None):
         """LayerNorm(x + sub)[row_index] in fp32, zero rows where row_index < 0.
 
         Not in the reference's surface: the scatter back from packed rows to
@@ -311,7 +357,7 @@ class Kernels:
         reference's final masked_fill. The residual sum is not stored.
         """
         _, out = self._layernorm("fused_add_layernorm", x, sub, weight, bias, eps, False,
-                                 write_xnew=False, row_index=row_index)
+                                 write_xnew=False, row_index=row_index, io=io)
         return out
 
     def fused_add_layernorm(self, x, sub, weight, bias, eps=1e-5, normed_half=False):
@@ -322,29 +368,40 @@ class Kernels:
                                         normed_half)
         return [x_new, normed]
 
-    def fused_add_layernorm_final(self, x, sub, weight, bias, eps=1e-5):
+    def fused_add_layernorm_final(self, x, sub, weight, bias, eps=1e-5, io=None):
         """LayerNorm(x + sub) only: the residual sum is not stored.
 
         For the model's last add+LN, whose sum nothing reads. Same kernel as
         fused_add_layernorm with the x_new store compiled out.
         """
         _, normed = self._layernorm("fused_add_layernorm", x, sub, weight, bias, eps, False,
-                                    write_xnew=False)
+                                    write_xnew=False, io=io)
         return normed
 
-    def fused_layernorm(self, x, weight, bias, eps=1e-5, out_half=False):
+    def fused_layernorm(self, x, weight, bias, eps=1e-5, out_half=False, io=None):
         """Plain LayerNorm over the last dimension."""
-        _, normed = self._layernorm("fused_layernorm", x, None, weight, bias, eps, out_half)
+        _, normed = self._layernorm("fused_layernorm", x, None, weight, bias, eps, out_half,
+                                    io=io)
         return normed
 
-    def fused_layernorm_split(self, x, weight, bias, eps=1e-5):
+    def fused_layernorm_copy(self, x, weight, bias, eps=1e-5, normed="float", io=None):
+        """[copy of x, LayerNorm(x)] from one read of x. Not in the reference's
+        surface: a captured graph's entry norm, which reads the caller's x
+        through the io slot and keeps the copy as the residual stream.
+        `normed` is "float", "half" or "split"."""
+        x_copy, out = self._layernorm("fused_layernorm", x, None, weight, bias, eps,
+                                      normed == "half", split=normed == "split", io=io,
+                                      copy_x=True)
+        return [x_copy, out]
+
+    def fused_layernorm_split(self, x, weight, bias, eps=1e-5, io=None):
         """LayerNorm as split fp16 planes [2, *x.shape]: hi, then lo = (v - hi) * 2^12.
 
         Not in the reference's surface: the input form of linear_bias_split,
         the fp32-class (fp16x3) projection. Same bytes as an fp32 output.
         """
         _, planes = self._layernorm("fused_layernorm", x, None, weight, bias, eps, False,
-                                    split=True)
+                                    split=True, io=io)
         return planes
 
     def fused_add_layernorm_split(self, x, sub, weight, bias, eps=1e-5):
@@ -373,7 +430,12 @@ class Kernels:
         if len(self._wcache) > 256:
             self._wcache = {k: v for k, v in self._wcache.items() if v[0]() is not None}
         self._wcache[id(weight)] = (weakref.ref(weight), key, hi, lo)
+        self._wcache_builds += 1
         return hi, lo
+
+    def cache_generation(self) -> int:
+        """Number of weight-cache entries built so far (it moves iff one was)."""
+        return self._wcache_builds
 
     def weight_cache_tensors(self) -> List[object]:
         """Every live cached fp16 weight buffer (graph capture pins these)."""
@@ -481,17 +543,38 @@ class Kernels:
 
     # -- attention (reference csrc/attention_dispatch.cuh:332-519) -------------------
 
+    def attention_split_plan(self, B, H, S, head_dim, is_causal=False, dtype=None,
+                             has_mask=False, rows=None, impl=0, precision=0, splits=0):
+        """(splits, workspace bytes) a call with these arguments resolves to.
+        `splits`: 0 the library's choice, 1 none, n forced. Not in the
+        reference's surface (its split choice is internal)."""
+        import torch
+
+        code = DOTL_F16 if dtype is None else _dtype_code(torch.empty(0, dtype=dtype))
+        n = ctypes.c_int32(1)
+        nbytes = ctypes.c_int64(0)
+        rows = B * S if rows is None else rows
+        self._check(self._lib.dotl_attention_split_plan(
+            int(B), int(H), int(S), int(head_dim), 1 if is_causal else 0, int(code),
+            1 if has_mask else 0, int(rows), int(impl), int(precision), int(splits),
+            ctypes.byref(n), ctypes.byref(nbytes)))
+        return int(n.value), int(nbytes.value)
+
     def fused_attention_forward(self, q, k, v, attn_mask=None, is_causal=False, scale=None,
                                 impl=0, out_layout=0, precision=0, cu_seqlens=None,
-                                max_seqlen=None):
+                                max_seqlen=None, splits=0):
         """softmax(q k^T * scale + mask) v (reference csrc/attention_dispatch.cuh:332-519).
 
-        q/k/v are [B, H, S, head_dim]. Beyond the reference's arguments:
-        with `cu_seqlens` (int32 [B + 1] on the device) they are packed
-        sequences instead, [rows, H, head_dim] with sequence b at rows
-        cu_seqlens[b] .. cu_seqlens[b + 1], `max_seqlen` (a host int) bounds
-        every sequence's length, there is no mask, and the output is
-        [rows, H * head_dim].
+        q/k/v are [B, H, S, head_dim] of float32, float16 or bfloat16. Beyond
+        the reference's arguments: with `cu_seqlens` (int32 [B + 1] on the
+        device) they are packed sequences instead, [rows, H, head_dim] with
+        sequence b at rows cu_seqlens[b] .. cu_seqlens[b + 1], `max_seqlen`
+        (a host int) must bound every sequence's length (rows of a longer one
+        past it are not computed), there is no mask, and the output is
+        [rows, H * head_dim]. `splits`: key-range splits for the fp16 MFMA
+        kernel (0 the library's choice from occupancy and the split knobs,
+        1 none, n forced); the partials' workspace comes from torch's
+        allocator on the current stream.
         """
         import torch
 
@@ -519,8 +602,8 @@ class Kernels:
         hd = int(q.shape[-1])
         if code is None:
             raise RuntimeError(f"{who}: impl={impl}, precision={precision} does not cover "
-                               f"dtype={q.dtype}, head_dim={hd}: the MFMA kernel takes float16 "
-                               f"or float32 tensors")
+                               f"dtype={q.dtype}, head_dim={hd}: the kernels take float16, "
+                               f"bfloat16 or float32 tensors")
         last = want_dim - 1
         pass_strided = (q.stride(last) == 1 and k.stride(last) == 1 and v.stride(last) == 1
                         and q.stride() == k.stride() and q.stride() == v.stride())
@@ -548,6 +631,7 @@ class Kernels:
                 B = 0
         else:
             B, H, S = (int(s) for s in q.shape[:3])
+            rows = B * S
             strides = (ctypes.c_int64 * 3)(q.stride(0), q.stride(1), q.stride(2))
             mask_ptr = None
             ms = None
@@ -562,11 +646,21 @@ class Kernels:
                 out = torch.empty((B, S, H * hd), dtype=q.dtype, device=q.device)
             else:
                 out = torch.empty((B, H, S, hd), dtype=q.dtype, device=q.device)
+        n_split, ws_bytes = 1, 0
+        if B and H and S:
+            n = ctypes.c_int32(1)
+            nb = ctypes.c_int64(0)
+            self._check(self._lib.dotl_attention_split_plan(
+                B, H, S, hd, 1 if is_causal else 0, code, 1 if mask_ptr else 0, rows,
+                int(impl), int(precision), int(splits), ctypes.byref(n), ctypes.byref(nb)))
+            n_split, ws_bytes = int(n.value), int(nb.value)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
         rc = self._lib.dotl_attention_forward(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), code,
             strides, mask_ptr, ms, out.data_ptr(), code,
             out_layout, B, H, S, hd, 1 if is_causal else 0, float(scale), int(impl),
-            int(precision), cu_ptr, self._stream(q.device))
+            int(precision), cu_ptr, rows, n_split, ws.data_ptr() if ws is not None else None,
+            ws_bytes, self._stream(q.device))
         self._check(rc)
         if rc == DOTL_DECLINED:
             raise RuntimeError(self._err())
@@ -667,16 +761,20 @@ class Kernels:
         return self._wmma_flags["direct_o"]
 
     def wmma_set_split_kv(self, on: bool) -> None:
-        self._wmma_flags["split_kv"] = bool(on)
+        """Let the MFMA kernel split the key range when the grid is small."""
+        self._lib.dotl_wmma_set_split_kv(1 if on else 0)
 
     def wmma_split_kv_enabled(self) -> bool:
-        return self._wmma_flags["split_kv"]
+        return bool(self._lib.dotl_wmma_split_kv_enabled())
 
     def wmma_set_split_count(self, n: int) -> None:
-        self._wmma_flags["split_count"] = int(n)
+        """Force n key splits on calls that leave the choice to the library
+        (0 restores the occupancy choice)."""
+        self._lib.dotl_wmma_set_split_count(int(n))
 
     def wmma_split_count(self, B, H, S, head_dim, is_causal) -> int:
-        return 1  # the MFMA kernel does not split the key range
+        """Key splits an fp16 call of this shape would run (1: none)."""
+        return self.attention_split_plan(B, H, S, head_dim, is_causal)[0]
 
     def wmma_set_causal_reverse(self, on: bool) -> None:
         self._wmma_flags["causal_reverse"] = bool(on)

@@ -32,6 +32,54 @@ fallback_counts: Counter = Counter()
 _fp16_pushed = None
 _cp_async_pushed = None
 
+# Set (to a graphs._GraphIO) only while a forward is being captured into a
+# hipGraph: the entry LayerNorm then reads the input, and the output
+# LayerNorm writes the output, through the graph's I/O slot.
+_graph_io = None
+
+
+# Set by OptimizedTransformer.forward for the duration of a forward of a
+# model with more than one block (config.STACK_PRECISION): rounding error
+# compounds through the residual stream from block to block, so a stack
+# spends more of its arithmetic on precision than one block needs.
+_stack_precision = False
+
+
+def _lb() -> str:
+    """config.LINEAR_BIAS as this forward applies it: "auto" becomes the split
+    fp16x3 arithmetic ("tf32") inside a multi-block forward."""
+    v = config.LINEAR_BIAS
+    return "tf32" if (v == "auto" and _stack_precision) else v
+
+
+def _lg() -> str:
+    """config.LINEAR_GELU as this forward applies it (see _lb)."""
+    v = config.LINEAR_GELU
+    return "tf32" if (v == "auto" and _stack_precision) else v
+
+
+def _input_io(x: torch.Tensor):
+    """io argument for a LayerNorm reading `x`: the slot when x is the input
+    of the forward being captured, else None."""
+    io = _graph_io
+    if io is not None and x is io.x_stand_in:
+        io.in_bound = True
+        return (io.slot, 1)
+    return None
+
+
+def _output_io():
+    """io argument for the forward's output LayerNorm while capturing."""
+    io = _graph_io
+    return (io.slot, 2) if io is not None else None
+
+
+def _note_output(out: torch.Tensor, io) -> torch.Tensor:
+    """Record which tensor stands for the slot-bound output."""
+    if io is not None and _graph_io is not None:
+        _graph_io.out_ptr = out.data_ptr()
+    return out
+
 
 def _sync_attention_precision(kernels) -> None:
     """Keep the extension's fp16 knob (what "auto" precision resolves to) in step."""
@@ -70,13 +118,49 @@ def _add_layernorm(x: torch.Tensor, sub: torch.Tensor, norm,
     return total, (out.half() if normed_half else out)
 
 
+def _add_layernorm_output(x: torch.Tensor, sub: torch.Tensor, norm) -> torch.Tensor:
+    """norm(x + sub) as the forward's output: the sum is not stored (nothing
+    reads it), and under capture the result goes through the graph's slot."""
+    kernels = _custom_kernels()
+    if kernels is not None:
+        io = _output_io()
+        return _note_output(kernels.fused_add_layernorm_final(x, sub, norm.weight, norm.bias,
+                                                              norm.eps, io=io), io)
+    fallback_counts["add_layernorm"] += 1
+    total = x + sub
+    return F.layer_norm(total, (total.shape[-1],), norm.weight, norm.bias, norm.eps)
+
+
+def _entry_norm(x: torch.Tensor, norm) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(residual stream, norm1(x)) for the model's first LayerNorm.
+
+    Normally the residual stream is x itself. While a graph is captured with
+    x bound to its I/O slot, the norm also writes a copy of x (from the same
+    read), and that copy is the residual stream: every later read of x then
+    happens inside the graph's own memory, so the bound input is read once.
+    """
+    io = _input_io(x) if config.LAYERNORM != "off" else None
+    if io is None:
+        return x, norm(x)
+    rows, width = x.numel() // x.shape[-1], x.shape[-1]
+    if _normed_split_wanted():
+        kind = "split"
+    elif _normed_wants_fp16(rows, width):
+        kind = "half"
+    else:
+        kind = "float"
+    x_copy, normed = _custom_kernels().fused_layernorm_copy(x, norm.weight, norm.bias,
+                                                           norm.eps, kind, io=io)
+    return x_copy, normed
+
+
 def _linear_gelu(x: torch.Tensor, lin, out_half: bool = False) -> torch.Tensor:
     """GELU_erf(lin(x)) with the GELU in the GEMM epilogue."""
-    if config.LINEAR_GELU != "off" and lin.bias is not None:
+    if _lg() != "off" and lin.bias is not None:
         kernels = _custom_kernels()
         if kernels is not None:
             out = kernels.linear_gelu(x, lin.weight, lin.bias, -1,
-                                      config._GEMM_MATH_CODE[config.LINEAR_GELU], out_half)
+                                      config._GEMM_MATH_CODE[_lg()], out_half)
             if out is not None:
                 return out
     fallback_counts["linear_gelu"] += 1
@@ -99,7 +183,7 @@ def _normed_split_wanted() -> bool:
     output in the same bytes as fp32, already in the form the MFMA passes
     read.
     """
-    return (config.LINEAR_BIAS == "auto" and config.QKV_PRECISION in ("fp16x3", "fp16x2")
+    return (_lb() == "auto" and config.QKV_PRECISION in ("fp16x3", "fp16x2")
             and config.NORMED_FP16 != "off")
 
 
@@ -155,7 +239,7 @@ def _layernorm_pack(x: torch.Tensor, norm, packing) -> Tuple[torch.Tensor, torch
     kernels = _custom_kernels()
     if kernels is not None:
         x_rows, normed = kernels.fused_layernorm_rows(x, norm.weight, norm.bias, packing.idx,
-                                                      norm.eps, kind, True)
+                                                      norm.eps, kind, True, io=_input_io(x))
         return x_rows, normed
     fallback_counts["layernorm"] += 1
     x_rows = x.reshape(-1, width).index_select(0, packing.idx.long())
@@ -175,9 +259,10 @@ def _add_layernorm_unpack(x: torch.Tensor, sub: torch.Tensor, norm, packing) -> 
     shape = (packing.batch, packing.seq_len, width)
     kernels = _custom_kernels()
     if kernels is not None:
+        io = _output_io()
         out = kernels.fused_add_layernorm_rows(x, sub, norm.weight, norm.bias, packing.inv,
-                                               norm.eps)
-        return out.view(shape)
+                                               norm.eps, io=io)
+        return _note_output(out, io).view(shape)
     fallback_counts["add_layernorm"] += 1
     y = F.layer_norm(x + sub, (width,), norm.weight, norm.bias, norm.eps)
     out = torch.zeros(packing.batch * packing.seq_len, width, dtype=y.dtype, device=y.device)
@@ -193,9 +278,10 @@ def _layernorm_unpack(x: torch.Tensor, norm, packing) -> torch.Tensor:
     shape = (packing.batch, packing.seq_len, width)
     kernels = _custom_kernels()
     if kernels is not None:
+        io = _output_io()
         _, out = kernels.fused_layernorm_rows(x, norm.weight, norm.bias, packing.inv, norm.eps,
-                                              "float", False)
-        return out.view(shape)
+                                              "float", False, io=io)
+        return _note_output(out, io).view(shape)
     fallback_counts["layernorm"] += 1
     y = F.layer_norm(x, (width,), norm.weight, norm.bias, norm.eps)
     out = torch.zeros(packing.batch * packing.seq_len, width, dtype=y.dtype, device=y.device)
@@ -203,12 +289,18 @@ def _layernorm_unpack(x: torch.Tensor, norm, packing) -> torch.Tensor:
     return out.view(shape)
 
 
-def _layernorm(x: torch.Tensor, norm, out_half: bool = False) -> torch.Tensor:
-    """LayerNorm(x) * w + b: the model's one norm with no residual before it."""
+def _layernorm(x: torch.Tensor, norm, out_half: bool = False,
+               output: bool = False) -> torch.Tensor:
+    """LayerNorm(x) * w + b: a norm with no residual add before it.
+
+    `output`: this is the forward's output norm (bound to the graph's I/O
+    slot while capturing)."""
     if config.LAYERNORM != "off":
         kernels = _custom_kernels()
         if kernels is not None:
-            return kernels.fused_layernorm(x, norm.weight, norm.bias, norm.eps, out_half)
+            io = _output_io() if output else None
+            return _note_output(kernels.fused_layernorm(x, norm.weight, norm.bias, norm.eps,
+                                                        out_half, io=io), io)
     fallback_counts["layernorm"] += 1
     out = F.layer_norm(x, (x.shape[-1],), norm.weight, norm.bias, norm.eps)
     return out.half() if out_half else out
@@ -225,7 +317,7 @@ def _attention_wants_fp16() -> bool:
 
 def _qkv_math_code() -> int:
     """linear_bias `math` for the QKV projection (config.QKV_PRECISION)."""
-    if config.LINEAR_BIAS == "tf32":
+    if _lb() == "tf32":
         return config._GEMM_MATH_CODE["tf32"]
     return config._QKV_MATH_CODE[config.QKV_PRECISION]
 
@@ -236,7 +328,7 @@ def _normed_wants_fp16(rows: int, width: int) -> bool:
     Only when that projection narrows its A operand to fp16 anyway: one-pass
     fp16 math. The split fp16x3 projection needs the fp32 values.
     """
-    if config.NORMED_FP16 == "off" or config.LINEAR_BIAS != "auto":
+    if config.NORMED_FP16 == "off" or _lb() != "auto":
         return False
     if _qkv_math_code() != -1:
         return False
@@ -247,7 +339,7 @@ def _normed_wants_fp16(rows: int, width: int) -> bool:
 
 def _gelu_input_wants_fp16(rows: int, width: int) -> bool:
     """Should norm2 emit fp16 for linear_gelu (which narrows A with the same RNE)?"""
-    if config.NORMED_FP16 == "off" or config.LINEAR_GELU != "auto":
+    if config.NORMED_FP16 == "off" or _lg() != "auto":
         return False
     if width > config._NORMED_FP16_MAX_K:
         return False
@@ -256,7 +348,7 @@ def _gelu_input_wants_fp16(rows: int, width: int) -> bool:
 
 def _gelu_output_wants_fp16(rows: int) -> bool:
     """Should linear_gelu store fp16 for ffn_out (whose fp16 math narrows it anyway)?"""
-    if config.GELU_FP16 == "off" or config.LINEAR_BIAS != "auto":
+    if config.GELU_FP16 == "off" or _lb() != "auto":
         return False
     return rows <= config._LINEAR_BIAS_MAX_ROWS
 
@@ -271,11 +363,11 @@ def _linear_bias(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Ten
     here, and counted as a fallback).
     """
     rows = x.numel() // x.shape[-1] if x.dim() >= 1 and x.shape[-1] else 0
-    if (config.LINEAR_BIAS != "off" and bias is not None
+    if (_lb() != "off" and bias is not None
             and rows <= config._LINEAR_BIAS_MAX_ROWS):
         kernels = _custom_kernels()
         if kernels is not None:
-            code = config._GEMM_MATH_CODE[config.LINEAR_BIAS] if math is None else math
+            code = config._GEMM_MATH_CODE[_lb()] if math is None else math
             out = kernels.linear_bias(x, weight, bias, -1, code, out_half, residual=residual)
             if out is not None:
                 return out
@@ -299,7 +391,7 @@ def _residual_epilogue_wanted(width_in: int) -> bool:
     multiple of 64), the add+LayerNorm after it then becomes a plain
     LayerNorm: one tensor read instead of two, none written back.
     """
-    return (config.RESIDUAL_EPILOGUE != "off" and config.LINEAR_BIAS == "auto"
+    return (config.RESIDUAL_EPILOGUE != "off" and _lb() == "auto"
             and width_in % 64 == 0 and width_in >= config._RESIDUAL_EPILOGUE_MIN_D)
 
 
@@ -307,7 +399,7 @@ def _ffn_block_eligible(x, ffn_in, ffn_out) -> bool:
     """Would _ffn_block run the fused kernel for this block (rather than decline)?"""
     if config.FFN_BLOCK == "off":
         return False
-    if (config.LINEAR_GELU != "auto" or config.LINEAR_BIAS != "auto"
+    if (_lg() != "auto" or _lb() != "auto"
             or config.NORMED_FP16 == "off" or config.GELU_FP16 == "off"):
         return False
     if ffn_in.bias is None or ffn_out.bias is None or x.dtype != torch.float32:
@@ -329,7 +421,7 @@ def _ffn_block(x, attn_out, norm1, ffn_in, ffn_out, norm2):
     """
     if config.FFN_BLOCK == "off":
         return None
-    if (config.LINEAR_GELU != "auto" or config.LINEAR_BIAS != "auto"
+    if (_lg() != "auto" or _lb() != "auto"
             or config.NORMED_FP16 == "off" or config.GELU_FP16 == "off"):
         return None
     if ffn_in.bias is None or ffn_out.bias is None or x.dtype != torch.float32:
@@ -345,6 +437,24 @@ def _ffn_block(x, attn_out, norm1, ffn_in, ffn_out, norm2):
     return (out[0], out[1]) if out else None
 
 
+
+def _attention_kernels():
+    """The loaded extension, synced with the attention knobs; raises without it.
+
+    Attention runs only on this build's own MFMA kernels: with libdotl_hip.so
+    absent there is nothing to run it on, and the call fails.
+    """
+    import kernel_ext
+
+    kernels = kernel_ext.get_kernels()
+    if kernels is None:
+        raise RuntimeError(f"attention needs libdotl_hip.so, which is not loaded "
+                           f"({kernel_ext.load_error()}); build it with "
+                           f"`python __graft_entry__.py` (hipcc, gfx950)")
+    _sync_attention_precision(kernels)
+    _sync_cp_async(kernels)
+    return kernels
+
 def _attention_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, packing,
                       is_causal: bool, scale: float) -> torch.Tensor:
     """Attention over packed sequences ([T_valid, H, hd] views) -> [T_valid, H*hd].
@@ -353,16 +463,7 @@ def _attention_packed(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, packing
     sized by the padded length S (not the longest valid one), so a captured
     graph depends on the packing's sizes only.
     """
-    import kernel_ext
-
-    kernels = kernel_ext.get_kernels()
-    if kernels is None:
-        raise RuntimeError(
-            "the gfx950 extension (libdotl_hip.so) failed to load, and there is no "
-            "fallback: this project implements attention itself and will not substitute "
-            f"a prebuilt one. Cause: {kernel_ext.load_error()}")
-    _sync_attention_precision(kernels)
-    _sync_cp_async(kernels)
+    kernels = _attention_kernels()
     return kernels.fused_attention_forward(
         q, k, v, None, is_causal, scale,
         config._IMPL_CODE[config.ATTENTION_IMPL], config._OUT_LAYOUT_BSHD,
@@ -379,16 +480,7 @@ def _attention_dispatch(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     attend) and `is_causal` may both be set: causal stays a flag so the kernel
     skips the tiles past the diagonal instead of masking them.
     """
-    import kernel_ext
-
-    kernels = kernel_ext.get_kernels()
-    if kernels is None:
-        raise RuntimeError(
-            "the gfx950 extension (libdotl_hip.so) failed to load, and there is no "
-            "fallback: this project implements attention itself and will not substitute "
-            f"a prebuilt one. Cause: {kernel_ext.load_error()}")
-    _sync_attention_precision(kernels)
-    _sync_cp_async(kernels)
+    kernels = _attention_kernels()
     return kernels.fused_attention_forward(
         q, k, v, attn_mask, is_causal, scale,
         config._IMPL_CODE[config.ATTENTION_IMPL],

@@ -13,7 +13,8 @@ import torch
 import torch.nn as nn
 
 from . import config
-from .kernels import (_add_layernorm, _add_layernorm_split, _add_layernorm_unpack,
+from .kernels import (_add_layernorm, _add_layernorm_output, _add_layernorm_split,
+                      _add_layernorm_unpack,
                       _attention_dispatch, _attention_packed, _attention_wants_fp16,
                       _ffn_block, _ffn_block_eligible, _gelu_input_wants_fp16,
                       _gelu_output_wants_fp16, _layernorm, _layernorm_split, _layernorm_unpack,
@@ -74,6 +75,7 @@ class MySelfAttention(nn.Module):
         self._qkv_key: Optional[Tuple] = None
         self._qkv_weight: Optional[torch.Tensor] = None
         self._qkv_bias: Optional[torch.Tensor] = None
+        self._qkv_generation = 0   # rebuild count (graph capture checks it)
 
     def _get_qkv_weight(self) -> Tuple[torch.Tensor, torch.Tensor]:
         """Q, K and V projections as one [3*d_model, d_model] GEMM operand.
@@ -92,6 +94,7 @@ class MySelfAttention(nn.Module):
                 self._qkv_bias = torch.cat([self.q_proj.bias, self.k_proj.bias,
                                             self.v_proj.bias], dim=0)
             self._qkv_key = key
+            self._qkv_generation += 1
         return self._qkv_weight, self._qkv_bias
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,
@@ -210,12 +213,18 @@ class MyTransformerBlock(nn.Module):
         if use_mask:
             # The reference zeroes padded rows between the add and the norm.
             x = (x + ffn_out).masked_fill(~valid_token_mask[..., None], 0)
-            return x, next_norm(x) if not next_norm_is_output else _final_norm(x, next_norm)
+            if not next_norm_is_output:
+                return x, next_norm(x)
+            # the model zeroes the padded rows of this norm's output again,
+            # so it is not the forward's output tensor
+            return x, _final_norm(x, next_norm, output=False)
 
-        if not next_norm_is_output and _normed_split_wanted():
+        if next_norm_is_output:
+            # the model's output: the residual sum is not stored
+            return None, _add_layernorm_output(x, ffn_out, next_norm)
+        if _normed_split_wanted():
             return _add_layernorm_split(x, ffn_out, next_norm)
-        trailing_half = (not next_norm_is_output
-                         and _normed_wants_fp16(rows, x.shape[-1]))
+        trailing_half = _normed_wants_fp16(rows, x.shape[-1])
         return _add_layernorm(x, ffn_out, next_norm, normed_half=trailing_half)
 
     def _residual_fused(self, x: torch.Tensor) -> bool:
@@ -270,6 +279,7 @@ class MyTransformerBlock(nn.Module):
                               normed_half=_normed_wants_fp16(rows, width))
 
 
-def _final_norm(x: torch.Tensor, norm: "MyLayerNorm") -> torch.Tensor:
-    """The model's output norm: never narrowed."""
-    return _layernorm(x, norm, out_half=False)
+def _final_norm(x: torch.Tensor, norm: "MyLayerNorm", output: bool = True) -> torch.Tensor:
+    """The model's output norm: never narrowed. `output`: its result is the
+    forward's output tensor (bound to a captured graph's output slot)."""
+    return _layernorm(x, norm, out_half=False, output=output)

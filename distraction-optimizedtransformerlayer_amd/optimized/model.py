@@ -1,7 +1,10 @@
-"""The optimized transformer (reference optimized/model.py:1-277)."""
+"""The optimized transformer (reference optimized/model.py:24-277 is the API kept:
+OptimizedTransformer, its forward, _forward_eager and the knob-driven graph
+and out-of-memory behaviour)."""
 
 from __future__ import annotations
 
+import math
 import weakref
 from typing import Dict, Optional, Tuple
 
@@ -9,11 +12,40 @@ import torch
 import torch.nn as nn
 
 from . import config
+from . import kernels as okernels
 from .graphs import _GraphRunner, _capture_graph, _graph_eligible, _graph_key, _graph_note_decline
-from .kernels import _layernorm_pack
+from .kernels import _entry_norm, _layernorm_pack
 from .layers import MyLayerNorm, MyTransformerBlock
 from .packing import RowPacking, build_packing
 from .util import _version_or_none
+
+
+def forward_bytes_per_token(d_model: int, ffn_dim: int, element_size: int) -> int:
+    """Device bytes one token holds at the forward's peak, from the layer's widths.
+
+    The peak is inside a block, after linear_gelu: the residual stream and
+    its next copy (x, h1), the normed planes, the fused qkv projection and
+    the attention context still referenced, and the FFN hidden activation.
+    Every 16-bit intermediate is counted at max(2, element size) and every
+    fp32 one at max(4, element size), so the bound holds for every dtype.
+    """
+    e32 = max(4, element_size)
+    e16 = max(2, element_size)
+    per_d = 4 * e32 + 3 * e16 + e16 + e32      # x, h1, normed planes (4 B), out; qkv; ctx; h2
+    return d_model * per_d + ffn_dim * e16
+
+
+def plan_batch_chunks(rows: int, bytes_per_row: int, free_bytes: int,
+                      min_chunks: int = 1) -> int:
+    """Number of equal batch chunks whose working set fits `free_bytes`.
+
+    At least `min_chunks` (the count an earlier out-of-memory forced), at
+    most one chunk per row.
+    """
+    if rows <= 1:
+        return 1
+    need = max(1, math.ceil(rows * bytes_per_row / max(1, free_bytes)))
+    return max(1, min(rows, max(need, min_chunks)))
 
 
 class OptimizedTransformer(nn.Module):
@@ -35,15 +67,17 @@ class OptimizedTransformer(nn.Module):
             for _ in range(config_.num_layers)
         ])
         self.final_norm = MyLayerNorm(config_.d_model)
-        # Trivial-mask memo, graph cache and chunk-size cache: plain
-        # attributes, out of state_dict().
+        # Host-side state, kept out of state_dict(): the mask memo, the
+        # graphs and what happened to each capture attempt, and the chunk
+        # counts out-of-memory retries settled on.
         self._triv_ref: Optional[weakref.ReferenceType] = None
         self._triv_version: Optional[int] = None
         self._packing: Optional[RowPacking] = None
         self._graphs: Dict[Tuple, _GraphRunner] = {}
-        self._graph_denied: set = set()
-        self._chunk_rows: Dict[Tuple, int] = {}
-        self._device_budget: Optional[int] = None
+        self._graph_log: Dict[Tuple, Dict] = {}
+        self._chunks: Dict[Tuple, int] = {}
+
+    # -- masks ---------------------------------------------------------------
 
     def _mask_packing(self, mask: Optional[torch.Tensor]) -> Optional[RowPacking]:
         """The mask's RowPacking, built once per mask object (one D2H sync).
@@ -68,6 +102,8 @@ class OptimizedTransformer(nn.Module):
         packing = self._mask_packing(mask)
         return packing is not None and packing.trivial
 
+    # -- the forward ---------------------------------------------------------
+
     def _forward_eager(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor],
                        use_mask: bool, packing: Optional[RowPacking] = None) -> torch.Tensor:
         """The whole model with every host decision already made: capturable.
@@ -79,7 +115,7 @@ class OptimizedTransformer(nn.Module):
         """
         if packing is not None:
             return self._forward_packed(x, packing)
-        normed = self.layers[0].norm1(x)
+        x, normed = _entry_norm(x, self.layers[0].norm1)
         last = len(self.layers) - 1
         for index, layer in enumerate(self.layers):
             next_norm = self.final_norm if index == last else self.layers[index + 1].norm1
@@ -102,13 +138,23 @@ class OptimizedTransformer(nn.Module):
 
     def forward(self, x: torch.Tensor,
                 valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        stacked = len(self.layers) > 1 and config.STACK_PRECISION == "auto"
+        saved = okernels._stack_precision
+        okernels._stack_precision = stacked
+        try:
+            return self._forward_dispatch(x, valid_token_mask)
+        finally:
+            okernels._stack_precision = saved
+
+    def _forward_dispatch(self, x: torch.Tensor,
+                          valid_token_mask: Optional[torch.Tensor]) -> torch.Tensor:
         packing = self._mask_packing(valid_token_mask)
         use_mask = packing is not None and not packing.trivial
         if not (use_mask and config.ROW_PACKING != "off" and x.is_cuda):
             packing = None
         key = _graph_key(x, use_mask, packing)
         runner = self._graphs.get(key)
-        if runner is None:
+        if runner is None and key not in self._graph_log:
             runner = self._maybe_capture(key, x, valid_token_mask, use_mask, packing)
         if runner is not None:
             return runner.replay(x, valid_token_mask, packing)
@@ -116,70 +162,95 @@ class OptimizedTransformer(nn.Module):
             return self._forward_chunk_on_oom(x, valid_token_mask, use_mask, packing)
         return self._forward_eager(x, valid_token_mask, use_mask, packing)
 
+    # -- memory pressure -----------------------------------------------------
+
+    def _free_device_bytes(self, x: torch.Tensor) -> int:
+        """Bytes the forward may plan to use on x's device: what is free now
+        (plus what torch's cache holds and can hand back), times the budget
+        fraction."""
+        free, _ = torch.cuda.mem_get_info(x.device)
+        reusable = torch.cuda.memory_reserved(x.device) - torch.cuda.memory_allocated(x.device)
+        return int((free + max(0, reusable)) * config._MICROBATCH_BUDGET_FRACTION)
+
     def _rows_within_budget(self, x: torch.Tensor) -> int:
-        """Batch rows whose predicted peak fits the device budget."""
-        rows = x.shape[0]
-        per_row = x.shape[1] * x.shape[2] * x.element_size() * config._MICROBATCH_PEAK_FACTOR
-        if per_row <= 0:
-            return rows
-        if self._device_budget is None:
-            _, total = torch.cuda.mem_get_info(x.device)
-            self._device_budget = int(total * config._MICROBATCH_BUDGET_FRACTION)
-        if per_row * rows <= self._device_budget:
-            return rows
-        return max(config._MICROBATCH_MIN_ROWS, min(rows, self._device_budget // per_row))
+        """Batch rows per chunk that the memory plan allows (x.shape[0] if all fit)."""
+        per_row = x.shape[1] * forward_bytes_per_token(x.shape[2], self.config.ffn_dim,
+                                                       x.element_size())
+        chunks = plan_batch_chunks(x.shape[0], per_row, self._free_device_bytes(x))
+        return max(config._MICROBATCH_MIN_ROWS, math.ceil(x.shape[0] / chunks))
 
     def _forward_chunk_on_oom(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor],
                               use_mask: bool,
                               packing: Optional[RowPacking] = None) -> torch.Tensor:
-        """_forward_eager, retried over halving batch chunks on out-of-memory.
+        """The eager forward over as many batch chunks as memory needs.
 
-        The chunk size that worked is cached per shape, so results stay stable
-        across calls (reference optimized/model.py:194-246). Chunks run the
-        padded path: a packing covers the whole batch.
+        The chunk count starts from a plan (the working set per sequence from
+        the layer's widths against the free device memory) and doubles after
+        every out-of-memory error until one sequence per chunk; the count
+        that worked is kept per shape. Sequences are independent, so each
+        chunk is a batch slice with its own rows of the mask (and its own
+        packing, rebuilt from that slice), written into one preallocated
+        output.
         """
-        rows = x.shape[0]
-        key = (rows, x.shape[1], x.shape[2], x.dtype, use_mask)
-        n = self._chunk_rows.get(key)
-        if n is None:
-            n = self._rows_within_budget(x)
-        if n >= rows:
+        B = x.shape[0]
+        key = (tuple(x.shape), x.dtype, use_mask, packing is not None)
+        chunks = self._chunks.get(key)
+        if chunks is None:
+            # planned once per shape (one device-memory query), then reused
+            per_row = x.shape[1] * forward_bytes_per_token(x.shape[2], self.config.ffn_dim,
+                                                           x.element_size())
+            chunks = plan_batch_chunks(B, per_row, self._free_device_bytes(x))
+            self._chunks[key] = chunks
+        while True:
             try:
-                return self._forward_eager(x, valid_token_mask, use_mask, packing)
+                if chunks == 1:
+                    return self._forward_eager(x, valid_token_mask, use_mask, packing)
+                return self._forward_in_chunks(x, valid_token_mask, use_mask,
+                                               packing is not None, chunks)
             except torch.OutOfMemoryError:
                 torch.cuda.empty_cache()
-                n = rows // 2
-        while n >= config._MICROBATCH_MIN_ROWS:
-            out = None
-            try:
-                out = torch.empty_like(x)
-                for lo in range(0, rows, n):
-                    hi = min(lo + n, rows)
-                    chunk_mask = valid_token_mask[lo:hi] if valid_token_mask is not None else None
-                    out[lo:hi] = self._forward_eager(x[lo:hi], chunk_mask, use_mask)
-                self._chunk_rows[key] = n
-                return out
-            except torch.OutOfMemoryError:
-                del out
-                torch.cuda.empty_cache()
-                if n <= config._MICROBATCH_MIN_ROWS:
+                if math.ceil(B / chunks) <= config._MICROBATCH_MIN_ROWS:
                     raise
-                n //= 2
-        return self._forward_eager(x, valid_token_mask, use_mask)
+                chunks = min(B, chunks * 2)
+                self._chunks[key] = chunks
+
+    def _forward_in_chunks(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor],
+                           use_mask: bool, packed: bool, chunks: int) -> torch.Tensor:
+        B = x.shape[0]
+        step = math.ceil(B / chunks)
+        out = None
+        for lo in range(0, B, step):
+            hi = min(B, lo + step)
+            part_mask = valid_token_mask[lo:hi] if valid_token_mask is not None else None
+            part_packing = None
+            if packed and part_mask is not None:
+                part_packing = build_packing(part_mask)
+                if part_packing.trivial:
+                    part_packing = None
+            part = self._forward_eager(x[lo:hi], part_mask, use_mask, part_packing)
+            if out is None:
+                out = torch.empty((B, *part.shape[1:]), dtype=part.dtype, device=part.device)
+            out[lo:hi] = part
+            del part
+        return out
+
+    # -- graphs --------------------------------------------------------------
 
     def _maybe_capture(self, key: Tuple, x: torch.Tensor,
-                       valid_token_mask: Optional[torch.Tensor],
-                       use_mask: bool,
+                       valid_token_mask: Optional[torch.Tensor], use_mask: bool,
                        packing: Optional[RowPacking] = None) -> Optional[_GraphRunner]:
-        """Capture a graph for this key, or decide not to (failures are remembered)."""
-        if key in self._graph_denied:
-            return None
+        """Try to capture a graph for `key`; every attempt's outcome is logged.
+
+        A key with an entry in `_graph_log` is never retried (forward checks
+        it before calling here); an ineligible call is not logged, so a later
+        change of config.CUDA_GRAPH is honoured.
+        """
         if not _graph_eligible(x, len(self._graphs)):
             _graph_note_decline(x)
             return None
-        runner = _capture_graph(self, x, valid_token_mask, use_mask, packing)
-        if runner is None:
-            self._graph_denied.add(key)
-            return None
-        self._graphs[key] = runner
+        log: Dict = {}
+        self._graph_log[key] = log
+        runner = _capture_graph(self, x, valid_token_mask, use_mask, packing, log=log)
+        if runner is not None:
+            self._graphs[key] = runner
         return runner

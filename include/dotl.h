@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DOTL_ABI_VERSION 2
+#define DOTL_ABI_VERSION 3
 
 #define DOTL_OK 0
 #define DOTL_DECLINED 1
@@ -48,6 +48,7 @@ extern "C" {
 #define DOTL_F16 1
 #define DOTL_F16X2 2 /* split fp16 planes [2][n]: hi = fp16(v), then
                         lo = fp16((v - hi) * 2^12); v ~= hi + lo * 2^-12 */
+#define DOTL_BF16 3  /* bfloat16 */
 
 /* linear activation codes */
 #define DOTL_ACT_NONE 0
@@ -87,29 +88,50 @@ int dotl_mfma_layout_probe(int32_t* out, void* stream);
  * Replaces fused_add_layernorm / fused_layernorm
  * (reference csrc/add_layernorm.cuh:491-692).
  *
- *   x, sub      [rows, D] contiguous, dtype DOTL_F32. sub == NULL: plain LN.
- *   weight,bias [D] float32
- *   x_new       [rows, D] float32 output, x + sub (rounded to fp32), or x alone
- *               when sub == NULL; may be NULL to skip the store
- *   normed      [rows, D] output of dtype normed_dtype (DOTL_F32; DOTL_F16, RNE
- *               narrowing; or DOTL_F16X2, [2][rows][D] split planes for the
- *               DOTL_MATH_FP16X3 GEMM), LayerNorm(x + sub) * weight + bias
+ *   x, sub      [rows, D] contiguous, dtype `dtype` (DOTL_F32, DOTL_F16 or
+ *               DOTL_BF16, the reference's float/Half/BFloat16 dispatch,
+ *               csrc/add_layernorm.cuh:555-557). sub == NULL: plain LN.
+ *   weight,bias [D], x's dtype
+ *   x_new       [rows, D] output of x's dtype, x + sub rounded to that dtype
+ *               (the value the statistics are taken of), or x alone when
+ *               sub == NULL; may be NULL to skip the store
+ *   normed      [rows, D] output, LayerNorm(x + sub) * weight + bias, of
+ *               dtype normed_dtype: x's dtype; or, for a float32 x only,
+ *               DOTL_F16 (RNE narrowing) or DOTL_F16X2 ([2][rows][D] split
+ *               planes for the split-arithmetic GEMMs)
  *   row_index   optional (NULL) int32 [rows]: output row t reads input row
  *               row_index[t] of x and sub ([in_rows, D] each), and an entry
  *               outside [0, in_rows) writes zeros to every output of row t.
- *               Without it, x and sub are [rows, D] and in_rows is ignored. Packs the valid rows of a padded batch
- *               (gather) and returns them to the padded layout with zeroed
- *               padding (scatter) -- the reference zeroes padded rows with
- *               masked_fill (reference optimized/layers.py:247-252,
- *               optimized/model.py:141-142); no reference counterpart of its own.
+ *               Without it, x and sub are [rows, D] and in_rows is ignored.
+ *               Packs the valid rows of a padded batch (gather) and returns
+ *               them to the padded layout with zeroed padding (scatter) --
+ *               the reference zeroes padded rows with masked_fill (reference
+ *               optimized/layers.py:247-252, optimized/model.py:141-142); no
+ *               reference counterpart of its own.
+ *   io, io_mode graph I/O slot, no reference counterpart: with bit 0 of
+ *               io_mode the kernel reads its x pointer from io[0] at run
+ *               time (x may then be NULL), with bit 1 its normed pointer from
+ *               io[1]. A captured graph then serves any input and output
+ *               buffer, rebound by dotl_bind_io before each replay, without
+ *               copies. io_mode 0: io unused (may be NULL).
  *   Statistics: fp32, mean then the centred sum of squares (biased variance),
  *   eps inside the square root.
  *   D in [1, 8192]; rows >= 0.
  */
-int dotl_layernorm(const void* x, const void* sub, const float* weight, const float* bias,
+int dotl_layernorm(const void* x, const void* sub, const void* weight, const void* bias,
                    void* x_new, void* normed, const int32_t* row_index, int64_t in_rows,
                    int64_t rows, int64_t D, double eps, int dtype, int normed_dtype,
-                   void* stream);
+                   const int64_t* io, int io_mode, void* stream);
+
+/*
+ * slot[0] = in, slot[1] = out, written by a one-wave kernel on `stream`, so
+ * the write is ordered before the graph replay launched after it. slot is a
+ * device int64 [2] that a captured graph's kernels read (dotl_layernorm's
+ * io). No reference counterpart: the reference copies each input into the
+ * captured graph's static buffer and clones its output
+ * (reference optimized/graphs.py:49-73).
+ */
+int dotl_bind_io(int64_t* slot, const void* in, void* out, void* stream);
 
 /*
  * Weight preparation for dotl_linear: w_hi = fp16(w) (RNE) and, when w_lo is
@@ -173,28 +195,45 @@ int dotl_linear_residual(const void* x, int x_dtype, const void* w_hi, const voi
  * Replaces fused_attention_forward
  * (reference csrc/attention_dispatch.cuh:332-519).
  *
- *   q, k, v      logical [B, H, S, head_dim], dtype DOTL_F16 or DOTL_F32
- *                (narrowed with RNE when staged), head_dim stride 1, and
- *                the (batch, head, seq) strides given once in qkv_strides[3]
- *                (in elements) for all three -- the strided views of a fused
- *                [B, S, 3, H, hd] projection pass through without copies.
+ *   q, k, v      logical [B, H, S, head_dim], dtype DOTL_F16, DOTL_BF16 or
+ *                DOTL_F32 (narrowed with RNE when staged), head_dim stride
+ *                1, and the (batch, head, seq) strides given once in
+ *                qkv_strides[3] (in elements) for all three -- the strided
+ *                views of a fused [B, S, 3, H, hd] projection pass through
+ *                without copies.
  *   mask         optional (NULL) bool bytes, true = may attend, addressed as
  *                mask[b*ms[0] + h*ms[1] + i*ms[2] + j*ms[3]] (expanded
  *                [B,H,S,S] strides; stride 0 on broadcast dims)
  *   out          out_layout 0: [B, H, S, head_dim]; 1: [B, S, H*head_dim];
- *                dtype out_dtype (DOTL_F16 or DOTL_F32)
+ *                dtype out_dtype (DOTL_F16 or DOTL_F32; DOTL_BF16 exactly
+ *                when q/k/v are bf16)
  *   is_causal    key j > query i is excluded (combinable with mask)
  *   impl         0 auto, 1 scalar, 2 wmma (here: the MFMA kernel), 3 tile
- *   precision    0 auto, 1 fp32, 2 tf32, 3 fp16, 4 bf16
+ *   precision    0 auto, 1 fp32, 2 tf32, 3 fp16, 4 bf16 (bf16 tensors
+ *                contract in bf16 on the MFMA kernel)
  *   cu_seqlens   optional (NULL) int32 [B + 1], non-decreasing, cu[0] = 0:
  *                packed sequences. Sequence b is rows [cu[b], cu[b+1]) of
  *                q/k/v (row stride qkv_strides[2], head stride
  *                qkv_strides[1]; qkv_strides[0] unused) and of out, which is
- *                then [cu[B], H*head_dim] (out_layout must be 1, mask NULL).
- *                S must be >= the longest sequence. This is the padded
- *                batch with its padding removed: no reference counterpart of
- *                its own (the reference masks padded keys,
+ *                then [rows, H*head_dim] (out_layout must be 1, mask NULL).
+ *                Contract: S >= every sequence's length (the grid is sized
+ *                from S; rows of a longer sequence past S are not written),
+ *                and rows == cu[B]. This is the padded batch with its
+ *                padding removed: no reference counterpart of its own (the
+ *                reference masks padded keys,
  *                reference csrc/attention_dispatch.cuh:404-450).
+ *   rows         with cu_seqlens, the packed row count cu[B] (q's first
+ *                dimension); ignored otherwise
+ *   splits       key-range splits (split-KV, the LDS-DMA kernel for fp16
+ *                q/k/v only; other kernels ignore it): 0 the library's
+ *                choice (dotl_wmma_set_split_count / dotl_wmma_set_split_kv,
+ *                else from occupancy), 1 none, n > 1 that many (at most one
+ *                per 64-key tile). Replaces the reference's split-KV path
+ *                (reference csrc/attention_wmma.cuh:706-759, 1783-1826).
+ *   workspace    device memory for the split partials, workspace_bytes long
+ *                (16-byte aligned): dotl_attention_split_plan says how many
+ *                bytes. Too small (or NULL) with splits = 0: the call runs
+ *                unsplit; with splits > 1: DOTL_E_INVALID.
  *   A query row with no allowed key produces 0.
  *   Returns DOTL_DECLINED when no kernel covers (dtype, head_dim); the caller
  *   raises, as the reference does.
@@ -204,7 +243,19 @@ int dotl_attention_forward(const void* q, const void* k, const void* v, int dtyp
                            const int64_t* mask_strides, void* out, int out_dtype,
                            int out_layout, int B, int H, int S, int head_dim,
                            int is_causal, double scale, int impl, int precision,
-                           const int32_t* cu_seqlens, void* stream);
+                           const int32_t* cu_seqlens, int64_t rows, int splits,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * The split count dotl_attention_forward would resolve `splits` (0, 1 or n)
+ * to for these arguments, and the workspace bytes it then needs (0 when it
+ * would not split). rows: B * S, or the packed row count. No device access.
+ * The counterpart of the reference's wmma_split_count
+ * (reference csrc/fused_attention.cu, csrc/attention_wmma.cuh:706-759).
+ */
+int dotl_attention_split_plan(int B, int H, int S, int head_dim, int is_causal, int dtype,
+                              int has_mask, int64_t rows, int impl, int precision, int splits,
+                              int* splits_out, int64_t* workspace_bytes_out);
 
 /*
  * Fused post-attention block. Replaces fused_ffn_block (reference
@@ -245,6 +296,12 @@ void dotl_wmma_set_fp16(int on);
 int dotl_wmma_fp16(void);
 void dotl_wmma_set_cp_async(int mode);
 int dotl_wmma_cp_async_mode(void);
+/* Split-KV knobs (reference wmma_set_split_kv / wmma_set_split_count): on
+ * (default) lets splits = 0 split from occupancy; a count n > 0 forces n
+ * splits for splits = 0 calls, 0 restores the occupancy choice. */
+void dotl_wmma_set_split_kv(int on);
+int dotl_wmma_split_kv_enabled(void);
+void dotl_wmma_set_split_count(int n);
 
 /* Measurement knob of the LDS-DMA attention kernel, no reference
  * counterpart: force its wavefronts per workgroup (1, 2, 4 or 8; 0 = by

@@ -101,14 +101,15 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, valid_keys=None,
     return out
 
 
-def layer(x: np.ndarray, valid: Optional[np.ndarray], params: Dict[str, np.ndarray],
-          num_heads: int, causal: bool) -> np.ndarray:
-    """One pre-LN block plus final norm, fp64, from the ops above."""
+def block(x: np.ndarray, valid: Optional[np.ndarray], params: Dict[str, np.ndarray],
+          prefix: str, num_heads: int, causal: bool) -> np.ndarray:
+    """One pre-LN block (BaselineTransformerBlock.forward, :234-245), fp64,
+    from the ops above: x + attn(norm1 x), + ffn(norm2 .), padded rows zeroed."""
     p = {k: np.asarray(v, dtype=np.float64) for k, v in params.items()}
     x = np.asarray(x, dtype=np.float64)
     B, S, D = x.shape
     hd = D // num_heads
-    pre = "layers.0."
+    pre = prefix
 
     def heads(t):
         return t.reshape(B, S, num_heads, hd).transpose(0, 2, 1, 3)
@@ -129,7 +130,24 @@ def layer(x: np.ndarray, valid: Optional[np.ndarray], params: Dict[str, np.ndarr
     h = h + f
     if valid is not None:
         h = np.where(valid[..., None], h, 0.0)
-    out = layer_norm(h, p["final_norm.weight"], p["final_norm.bias"])
+    return h
+
+
+def model(x: np.ndarray, valid: Optional[np.ndarray], params: Dict[str, np.ndarray],
+          num_heads: int, causal: bool, num_layers: int = 1) -> np.ndarray:
+    """`num_layers` blocks (layers.0. .. layers.{L-1}.), then the final norm
+    and the padded-row zeroing (BaselineTransformer.forward, :262-272)."""
+    h = np.asarray(x, dtype=np.float64)
+    for i in range(num_layers):
+        h = block(h, valid, params, f"layers.{i}.", num_heads, causal)
+    out = layer_norm(h, np.asarray(params["final_norm.weight"], dtype=np.float64),
+                     np.asarray(params["final_norm.bias"], dtype=np.float64))
     if valid is not None:
         out = np.where(valid[..., None], out, 0.0)
     return out
+
+
+def layer(x: np.ndarray, valid: Optional[np.ndarray], params: Dict[str, np.ndarray],
+          num_heads: int, causal: bool) -> np.ndarray:
+    """One pre-LN block plus final norm, fp64, from the ops above."""
+    return model(x, valid, params, num_heads, causal, 1)

@@ -160,9 +160,15 @@ def attention_useful_flops(cfg: LayerConfig, lengths: np.ndarray) -> float:
     return 4.0 * cfg.head_dim * cfg.num_heads * float(pairs.sum())
 
 
-def gemm_flops(cfg: LayerConfig) -> float:
-    """8 T D^2 + 4 T D F: QKV (6TD^2) + out_proj (2TD^2) + two FFN GEMMs."""
-    T, D, F = cfg.tokens, cfg.d_model, cfg.ffn_dim
+def gemm_flops(cfg: LayerConfig, rows: Optional[int] = None) -> float:
+    """8 T D^2 + 4 T D F: QKV (6TD^2) + out_proj (2TD^2) + two FFN GEMMs.
+
+    `rows` replaces T = B*S by the number of rows that carry work: a padded
+    batch's valid rows (sum of the lengths), the rows whose outputs survive
+    the reference's masked_fill of padded rows.
+    """
+    T = cfg.tokens if rows is None else int(rows)
+    D, F = cfg.d_model, cfg.ffn_dim
     return 8.0 * T * D * D + 4.0 * T * D * F
 
 
@@ -170,3 +176,38 @@ def layernorm_bytes(cfg: LayerConfig, normed_bytes: int = 4) -> float:
     """One plain LN (read x, write normed) + two add+LN (read x, sub; write x_new, normed)."""
     T, D = cfg.tokens, cfg.d_model
     return float(T * D * ((4 + normed_bytes) + 2 * (12 + normed_bytes)))
+
+
+def stack_layers(params: Dict[str, np.ndarray], num_layers: int,
+                 seed: Optional[int] = None) -> Dict[str, np.ndarray]:
+    """A `num_layers`-block weight dict whose block 0 and final norm are `params`'.
+
+    Blocks 1 .. L-1 get their own Xavier-uniform weights (zero biases, unit /
+    zero LayerNorm affine, as block 0 under the configs' spec), drawn from a
+    PCG64 stream seeded by `seed` (default: derived from block 0's first
+    weight, so a config always stacks the same way). Key names follow the
+    reference's state_dict (layers.{i}.*).
+    """
+    if num_layers == 1:
+        return dict(params)
+    wq0 = params["layers.0.attention.q_proj.weight"]
+    D = wq0.shape[0]
+    F = params["layers.0.ffn_in.weight"].shape[0]
+    if seed is None:
+        seed = SEED_BASE + int(np.float64(wq0[0, 0]).view(np.uint64) % (1 << 31))
+    rng = np.random.Generator(np.random.PCG64(seed))
+    out = dict(params)
+    for i in range(1, num_layers):
+        pre = f"layers.{i}."
+        out[pre + "norm1.weight"] = np.ones(D, dtype=np.float32)
+        out[pre + "norm1.bias"] = np.zeros(D, dtype=np.float32)
+        for name in ("q_proj", "k_proj", "v_proj", "out_proj"):
+            out[pre + f"attention.{name}.weight"] = xavier_uniform(rng, D, D)
+            out[pre + f"attention.{name}.bias"] = np.zeros(D, dtype=np.float32)
+        out[pre + "norm2.weight"] = np.ones(D, dtype=np.float32)
+        out[pre + "norm2.bias"] = np.zeros(D, dtype=np.float32)
+        out[pre + "ffn_in.weight"] = xavier_uniform(rng, F, D)
+        out[pre + "ffn_in.bias"] = np.zeros(F, dtype=np.float32)
+        out[pre + "ffn_out.weight"] = xavier_uniform(rng, D, F)
+        out[pre + "ffn_out.bias"] = np.zeros(D, dtype=np.float32)
+    return out

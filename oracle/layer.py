@@ -1,14 +1,14 @@
 """The reference layer, restated on the CPU in torch.
 
-Follows BaselineTransformer with num_layers=1 op for op
-(torch_transformer_benchmark.py):
+Follows BaselineTransformer op for op, for as many blocks as the weight dict
+holds (torch_transformer_benchmark.py):
 
   attention   :96-133   q/k/v projections, split heads, scores * hd^-1/2,
                         causal triu(1) -> -inf, key mask -> -inf, fp32 softmax,
                         P @ V, merge heads, out_proj, masked_fill padded rows
   block       :234-245  x + attn(norm1(x)); x + ffn_out(gelu_erf(ffn_in(norm2(x))));
                         masked_fill padded rows
-  model       :262-272  blocks, final_norm, masked_fill padded rows
+  model       :262-272  every block in order, final_norm, masked_fill padded rows
 
 The reference arithmetic is PyTorch's own (nn.Linear, nn.LayerNorm,
 torch.matmul, torch.softmax, F.gelu), so the restatement calls the same
@@ -85,12 +85,19 @@ def attention(x: torch.Tensor, p: Dict[str, torch.Tensor], prefix: str,
     return out
 
 
+def num_layers_of(params: Dict) -> int:
+    """Blocks a state dict holds (layers.0. .. layers.{L-1}.)."""
+    return 1 + max(int(k.split(".")[1]) for k in params if k.startswith("layers."))
+
+
 def reference_layer(x, valid, params, cfg: LayerConfig, dtype=torch.float32,
                     norm_first: bool = True, threads: Optional[int] = None) -> torch.Tensor:
-    """BaselineTransformer(num_layers=1).forward(x, valid) on the CPU.
+    """BaselineTransformer.forward(x, valid) on the CPU.
 
     x       [B, S, D] array or tensor; valid [B, S] bool or None
-    params  name -> array, keyed as the reference's state_dict
+    params  name -> array, keyed as the reference's state_dict; every block
+            it holds (layers.0. .. layers.{L-1}.) runs, in order, then the
+            final norm (reference :262-272)
     returns [B, S, D] tensor of `dtype`
     """
     if threads is not None:
@@ -99,21 +106,24 @@ def reference_layer(x, valid, params, cfg: LayerConfig, dtype=torch.float32,
         p = {k: _t(v, dtype) for k, v in params.items()}
         h = _t(x, dtype)
         m = None if valid is None else _t(valid, torch.bool)
-        pre = "layers.0."
-        if norm_first:
-            h = h + attention(layer_norm(h, p[pre + "norm1.weight"], p[pre + "norm1.bias"]),
-                              p, pre + "attention.", cfg.num_heads, m, cfg.causal)
-            n2 = layer_norm(h, p[pre + "norm2.weight"], p[pre + "norm2.bias"])
-            h = h + linear(gelu(linear(n2, p[pre + "ffn_in.weight"], p[pre + "ffn_in.bias"])),
+        for i in range(num_layers_of(params)):
+            pre = f"layers.{i}."
+            if norm_first:
+                h = h + attention(layer_norm(h, p[pre + "norm1.weight"], p[pre + "norm1.bias"]),
+                                  p, pre + "attention.", cfg.num_heads, m, cfg.causal)
+                n2 = layer_norm(h, p[pre + "norm2.weight"], p[pre + "norm2.bias"])
+                h = h + linear(gelu(linear(n2, p[pre + "ffn_in.weight"],
+                                           p[pre + "ffn_in.bias"])),
+                               p[pre + "ffn_out.weight"], p[pre + "ffn_out.bias"])
+            else:
+                h = layer_norm(h + attention(h, p, pre + "attention.", cfg.num_heads, m,
+                                             cfg.causal),
+                               p[pre + "norm1.weight"], p[pre + "norm1.bias"])
+                f = linear(gelu(linear(h, p[pre + "ffn_in.weight"], p[pre + "ffn_in.bias"])),
                            p[pre + "ffn_out.weight"], p[pre + "ffn_out.bias"])
-        else:
-            h = layer_norm(h + attention(h, p, pre + "attention.", cfg.num_heads, m, cfg.causal),
-                           p[pre + "norm1.weight"], p[pre + "norm1.bias"])
-            f = linear(gelu(linear(h, p[pre + "ffn_in.weight"], p[pre + "ffn_in.bias"])),
-                       p[pre + "ffn_out.weight"], p[pre + "ffn_out.bias"])
-            h = layer_norm(h + f, p[pre + "norm2.weight"], p[pre + "norm2.bias"])
-        if m is not None:
-            h = h.masked_fill(~m[..., None], 0)
+                h = layer_norm(h + f, p[pre + "norm2.weight"], p[pre + "norm2.bias"])
+            if m is not None:
+                h = h.masked_fill(~m[..., None], 0)
         out = layer_norm(h, p["final_norm.weight"], p["final_norm.bias"])
         if m is not None:
             out = out.masked_fill(~m[..., None], 0)

@@ -42,7 +42,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_and_target(lib):
-    assert lib.dotl_abi_version() == 2
+    assert lib.dotl_abi_version() == 3
     assert lib.dotl_target() == b"gfx950"
 
 
@@ -77,10 +77,57 @@ def _attn(lib, **kw):
     args.update(kw)
     strides = (ctypes.c_int64 * 3)(0, 0, 0)
     return lib.dotl_attention_forward(None, None, None, args["dtype"], strides, None, None,
-                                      None, args["dtype"], args["out_layout"], args["B"],
-                                      args["H"], args["S"], args["hd"], args["causal"],
-                                      ctypes.c_double(0.125), args["impl"], args["prec"],
-                                      args.get("cu"), None)
+                                      None, args.get("out_dtype", args["dtype"]),
+                                      args["out_layout"], args["B"], args["H"], args["S"],
+                                      args["hd"], args["causal"], ctypes.c_double(0.125),
+                                      args["impl"], args["prec"], args.get("cu"),
+                                      args.get("rows", 0), args.get("splits", 0),
+                                      args.get("ws"), args.get("ws_bytes", 0), None)
+
+
+def _plan(lib, B=1, H=8, S=2048, hd=64, dtype=1, mask=0, rows=None, splits=0, impl=0, prec=0):
+    n = ctypes.c_int32(0)
+    nb = ctypes.c_int64(0)
+    rc = lib.dotl_attention_split_plan(B, H, S, hd, 0, dtype, mask, B * S if rows is None else rows,
+                                       impl, prec, splits, ctypes.byref(n), ctypes.byref(nb))
+    return rc, n.value, nb.value
+
+
+def test_split_plan(lib):
+    """Split-KV is chosen from occupancy for the fp16 MFMA kernel only, and
+    sized as splits x rows x heads x (head_dim fp32 + (max, sum))."""
+    lib.dotl_wmma_set_split_kv(1)
+    lib.dotl_wmma_set_split_count(0)
+    # B=1, H=8, S=2048: 16 query blocks x 8 heads = 128 workgroups -> 4 splits of 8 tiles
+    rc, n, nb = _plan(lib)
+    assert rc == 0 and n == 4 and nb == 4 * 2048 * 8 * (64 * 4 + 8)
+    # a full grid (C4: 4 x 16 heads x 8 blocks of 256 queries) does not split
+    assert _plan(lib, B=4, H=16, S=2048, hd=128)[1] == 1
+    # short sequences run the one-tile kernel, never split unless forced
+    assert _plan(lib, B=1, H=1, S=32)[1] == 1
+    # fp32 / bf16 tensors and the exact kernel do not split
+    assert _plan(lib, dtype=0)[1] == 1 and _plan(lib, dtype=3)[1] == 1
+    assert _plan(lib, impl=1)[1] == 1
+    # forcing: capped at one split per 64-key tile, rounded so no split is empty
+    assert _plan(lib, S=256, splits=8)[1] == 4
+    assert _plan(lib, S=2048, splits=3)[1] == 3
+    assert _plan(lib, splits=1)[1:] == (1, 0)
+    # the knobs: a forced count, and off
+    lib.dotl_wmma_set_split_count(2)
+    assert _plan(lib, B=4, H=16, S=2048, hd=128)[1] == 2
+    lib.dotl_wmma_set_split_count(0)
+    lib.dotl_wmma_set_split_kv(0)
+    assert _plan(lib)[1] == 1
+    assert _plan(lib, splits=4)[1] == 4       # an explicit count is not a knob's choice
+    lib.dotl_wmma_set_split_kv(1)
+
+
+def test_split_needs_its_workspace(lib):
+    # forced splits with no workspace is an error; auto would run unsplit
+    assert _attn(lib, B=1, H=8, S=2048, hd=64, splits=4) == -1
+    assert b"workspace" in lib.dotl_last_error()
+    assert _attn(lib, B=1, H=8, S=2048, hd=64, splits=0) == -1   # then the null tensors
+    assert b"null pointer" in lib.dotl_last_error()
 
 
 def test_attention_vocabulary_checks(lib):
@@ -115,15 +162,33 @@ def test_attention_vocabulary_checks(lib):
 
 
 def test_layernorm_checks(lib):
-    def ln(rows, D, dtype=0, row_index=None, in_rows=0):
+    def ln(rows, D, dtype=0, normed=None, row_index=None, in_rows=0, io=None, io_mode=0):
         return lib.dotl_layernorm(None, None, None, None, None, None, row_index, in_rows, rows, D,
-                                  ctypes.c_double(1e-5), dtype, 0, None)
+                                  ctypes.c_double(1e-5), dtype,
+                                  dtype if normed is None else normed, io, io_mode, None)
 
     assert ln(4, 0) == -1        # D = 0
     assert ln(0, 64) == 0        # no rows
-    assert ln(4, 64, dtype=1) == 1   # fp16 input declined
+    assert ln(4, 64, dtype=7) == -1       # unknown dtype
+    # fp16 / bf16 inputs take their own dtype as the normed output
+    assert ln(0, 64, dtype=1) == 0 and ln(0, 64, dtype=3) == 0
+    assert ln(4, 64, dtype=3, normed=1) == -1
+    assert b"x's dtype" in lib.dotl_last_error()
+    assert ln(4, 64, dtype=1, normed=2) == -1   # split planes only from fp32
     idx = (ctypes.c_int32 * 1)(0)
     assert ln(1, 64, row_index=ctypes.cast(idx, ctypes.c_void_p), in_rows=-1) == -1
+    # an io mode needs a slot; modes past 3 do not exist
+    assert ln(4, 64, io_mode=1) == -1
+    slot = (ctypes.c_int64 * 2)(0, 0)
+    assert ln(4, 64, io=ctypes.cast(slot, ctypes.c_void_p), io_mode=4) == -1
+    # null tensors that no slot replaces are an error
+    assert ln(4, 64, io=ctypes.cast(slot, ctypes.c_void_p), io_mode=1) == -1
+    assert b"null pointer" in lib.dotl_last_error()
+
+
+def test_bind_io_checks(lib):
+    assert lib.dotl_bind_io(None, None, None, None) == -1
+    assert b"null slot" in lib.dotl_last_error()
 
 
 def test_ffn_block_checks(lib):

@@ -353,9 +353,9 @@ def test_attention_refusals(kernels):
         # would run the exact fp32 kernel instead)
         q48 = torch.randn(1, 1, 16, 48, device=DEV).half()
         kernels.fused_attention_forward(q48, q48, q48, None, False, 0.125, 2, 1, 0)
-    with pytest.raises(RuntimeError):
-        qb = q.bfloat16()
-        kernels.fused_attention_forward(qb, qb, qb, None, False, 0.125, 0, 1, 0)
+    with pytest.raises(RuntimeError, match="float16, bfloat16 or float32"):
+        qi = torch.zeros(1, 1, 16, 64, dtype=torch.float64, device=DEV)
+        kernels.fused_attention_forward(qi, qi, qi, None, False, 0.125, 0, 1, 0)
 
 
 # ---- LDS-DMA pipelined GEMM --------------------------------------------------------

@@ -13,8 +13,10 @@ import torch
 
 from oracle import brute
 from oracle.compare import compare_outputs, element_ok
-from oracle.inputs import CONFIGS, LayerConfig, attention_useful_flops, gemm_flops, make_case
-from oracle.layer import attention, gelu, layer_norm, linear, reference_attention, reference_layer
+from oracle.inputs import (CONFIGS, LayerConfig, attention_useful_flops, gemm_flops, make_case,
+                           stack_layers)
+from oracle.layer import (attention, gelu, layer_norm, linear, num_layers_of, reference_attention,
+                          reference_layer)
 
 TINY = LayerConfig("tiny", 2, 5, 8, 2, 12, False, "keypad", 2, 1.0, 99)
 TINY_CAUSAL = LayerConfig("tinyc", 2, 6, 8, 2, 16, True, "none", 6, 1.0, 98)
@@ -158,6 +160,48 @@ def test_layer_matches_brute_force(cfg, affine):
     np.testing.assert_allclose(got32, want, atol=2e-5)
     if mask is not None:
         assert np.all(got32[~mask] == 0.0)  # padded rows are exactly zero
+
+
+@pytest.mark.parametrize("cfg", [TINY, TINY_CAUSAL], ids=["keypad", "causal"])
+def test_multi_layer_matches_chained_brute_force_blocks(cfg):
+    """L blocks then the final norm: the fp64 oracle equals fp64 brute-force
+    blocks chained by hand, and each block and its order matter."""
+    x, mask, params = make_case(cfg, nonzero_affine=True)
+    p3 = stack_layers(params, 3)
+    assert num_layers_of(p3) == 3
+    for k, v in params.items():            # block 0 and the final norm are kept
+        assert np.array_equal(p3[k], v)
+    h = x.astype(np.float64)
+    for i in range(3):
+        h = brute.block(h, mask, p3, f"layers.{i}.", cfg.num_heads, cfg.causal)
+    want = brute.layer_norm(h, p3["final_norm.weight"].astype(np.float64),
+                            p3["final_norm.bias"].astype(np.float64))
+    if mask is not None:
+        want = np.where(mask[..., None], want, 0.0)
+    got = reference_layer(x, mask, p3, cfg, dtype=torch.float64).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(brute.model(x, mask, p3, cfg.num_heads, cfg.causal, 3), want,
+                               rtol=1e-12, atol=1e-12)
+    # two blocks, or the blocks swapped, give a different answer
+    two = reference_layer(x, mask, stack_layers(params, 2), cfg, dtype=torch.float64).numpy()
+    assert np.abs(two - got).max() > 1e-3
+    swapped = dict(p3)
+    for k in [k for k in p3 if k.startswith("layers.1.")]:
+        swapped[k], swapped["layers.2." + k[9:]] = p3["layers.2." + k[9:]], p3[k]
+    sw = reference_layer(x, mask, swapped, cfg, dtype=torch.float64).numpy()
+    assert np.abs(sw - got).max() > 1e-3
+
+
+def test_stack_layers_is_deterministic_and_xavier():
+    _, _, params = make_case(TINY)
+    a, b = stack_layers(params, 4), stack_layers(params, 4)
+    assert all(np.array_equal(a[k], b[k]) for k in a)
+    D = params["layers.0.norm1.weight"].shape[0]
+    F = params["layers.0.ffn_in.weight"].shape[0]
+    bound = np.sqrt(6.0 / (D + F))
+    assert np.abs(a["layers.3.ffn_in.weight"]).max() <= bound
+    assert not np.array_equal(a["layers.1.attention.q_proj.weight"],
+                              a["layers.2.attention.q_proj.weight"])
 
 
 def test_layer_residual_and_final_norm_are_present():
