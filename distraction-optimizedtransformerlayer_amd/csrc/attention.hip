@@ -40,6 +40,7 @@
 #include "attention_params.h"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace dotl {
@@ -730,4 +731,102 @@ extern "C" int dotl_attention_forward(const void* q, const void* k, const void* 
         return DOTL_E_INVALID;
     }
     return check_launch("fused_attention_forward");
+}
+
+// ---- no-allocation entry point --------------------------------------------
+//
+// dotl_attention_forward_noalloc: dotl_attention_forward with the split-KV
+// partials in a fixed device array of this library instead of a caller
+// workspace, for callers that cannot allocate (code under stream capture,
+// serving loops that forbid hipMalloc). Every call on one GPU shares that
+// GPU's copy of the array; calls that overlap on one GPU race on it.
+namespace dotl {
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = 32ll << 20;
+constexpr int kMaxDevices = 64;
+
+// The scratch memory. In host code `scratch` names a host-side stand-in, not
+// a device address: only the pointer hipGetSymbolAddress returns for the
+// current device (kept in g_scratch_ptr) is ever handed to a kernel.
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's scratch address, resolved on the first call on the device
+// (with that device current) and kept; nullptr with the error set on failure.
+void* scratch_for_current_device() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("fused_attention_forward_noalloc: no current HIP device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || ptr == nullptr) {
+            set_error(std::string("fused_attention_forward_noalloc: hipGetSymbolAddress failed: ") +
+                      hipGetErrorString(err));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace dotl
+
+extern "C" int64_t dotl_attention_noalloc_scratch_bytes(void) {
+    return dotl::kNoAllocScratchBytes;
+}
+
+extern "C" int dotl_attention_forward_noalloc(const void* q, const void* k, const void* v,
+                                              int dtype, const int64_t* qkv_strides,
+                                              const uint8_t* mask, const int64_t* mask_strides,
+                                              void* out, int out_dtype, int out_layout, int B,
+                                              int H, int S, int head_dim, int is_causal,
+                                              double scale, int impl, int precision,
+                                              const int32_t* cu_seqlens, int64_t rows,
+                                              int splits, void* stream) {
+    using namespace dotl;
+    clear_error();
+    DOTL_REQUIRE(splits >= 0, "fused_attention_forward_noalloc: negative split count");
+    const int64_t part_rows = cu_seqlens != nullptr ? rows : static_cast<int64_t>(B) * S;
+    // The split count the allocating entry would run, fitted to the scratch:
+    // a library choice (splits = 0) drops to the largest count that fits (one
+    // split needs no scratch); an explicit count that does not fit is refused.
+    int n = 1;
+    int64_t need = 0;
+    int rc = dotl_attention_split_plan(B, H, S, head_dim, is_causal, dtype, mask != nullptr,
+                                       part_rows, impl, precision, splits, &n, &need);
+    if (rc != DOTL_OK) return rc;
+    if (need > kNoAllocScratchBytes) {
+        if (splits > 1) {
+            char buf[256];
+            std::snprintf(buf, sizeof(buf),
+                          "fused_attention_forward_noalloc: %d key splits need %lld bytes of "
+                          "scratch, over the %lld bytes this entry point holds per device; ask "
+                          "for fewer splits or use dotl_attention_forward with a workspace",
+                          n, static_cast<long long>(need),
+                          static_cast<long long>(kNoAllocScratchBytes));
+            set_error(buf);
+            return DOTL_E_INVALID;
+        }
+        while (n > 1 && attn_split_workspace_bytes(part_rows, H, head_dim, n) >
+                            kNoAllocScratchBytes) {
+            --n;
+        }
+    }
+    void* ws = nullptr;
+    if (n > 1) {
+        ws = scratch_for_current_device();
+        if (ws == nullptr) return DOTL_E_LAUNCH;
+    }
+    return dotl_attention_forward(q, k, v, dtype, qkv_strides, mask, mask_strides, out, out_dtype,
+                                  out_layout, B, H, S, head_dim, is_causal, scale, impl, precision,
+                                  cu_seqlens, rows, n, ws, n > 1 ? kNoAllocScratchBytes : 0,
+                                  stream);
 }

@@ -59,7 +59,8 @@ EXPORTED_SYMBOLS = (
     "dotl_wmma_set_cp_async", "dotl_wmma_cp_async_mode", "dotl_lds_dma_probe",
     "dotl_attention_set_pipeline", "dotl_linear_residual", "dotl_bind_io",
     "dotl_attention_split_plan", "dotl_wmma_set_split_kv", "dotl_wmma_split_kv_enabled",
-    "dotl_wmma_set_split_count",
+    "dotl_wmma_set_split_count", "dotl_attention_forward_noalloc",
+    "dotl_attention_noalloc_scratch_bytes",
 )
 
 _kernels = None
@@ -119,6 +120,13 @@ def _declare(lib) -> None:
     lib.dotl_attention_forward.argtypes = [vp, vp, vp, i32, c.POINTER(i64), vp, c.POINTER(i64),
                                            vp, i32, i32, i32, i32, i32, i32, i32, c.c_double,
                                            i32, i32, vp, i64, i32, vp, i64, vp]
+    lib.dotl_attention_forward_noalloc.restype = i32
+    lib.dotl_attention_forward_noalloc.argtypes = [vp, vp, vp, i32, c.POINTER(i64), vp,
+                                                   c.POINTER(i64), vp, i32, i32, i32, i32, i32,
+                                                   i32, i32, c.c_double, i32, i32, vp, i64, i32,
+                                                   vp]
+    lib.dotl_attention_noalloc_scratch_bytes.restype = i64
+    lib.dotl_attention_noalloc_scratch_bytes.argtypes = []
     lib.dotl_attention_split_plan.restype = i32
     lib.dotl_attention_split_plan.argtypes = [i32, i32, i32, i32, i32, i32, i32, i64, i32, i32,
                                               i32, c.POINTER(i32), c.POINTER(i64)]

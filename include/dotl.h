@@ -247,6 +247,32 @@ int dotl_attention_forward(const void* q, const void* k, const void* v, int dtyp
                            void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * dotl_attention_forward that allocates nothing: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under
+ * hipGraph stream capture, serving loops or harnesses that forbid hipMalloc).
+ * Same arguments and results as dotl_attention_forward minus the workspace:
+ * the split-KV partials live in a fixed array of this library, one per GPU,
+ * of dotl_attention_noalloc_scratch_bytes() bytes (32 MiB), held until the
+ * process ends; its address is resolved on the first call on each device
+ * (make that first call outside stream capture). splits = 0 runs the largest
+ * split count up to the library's choice that fits the array; an explicit
+ * splits > 1 that does not fit returns DOTL_E_INVALID. Nothing in the array
+ * needs to start at zero (every partial the combine reads is written first
+ * by the same call). Calls that overlap on one GPU (concurrent streams)
+ * race on the array: serialise them.
+ */
+int dotl_attention_forward_noalloc(const void* q, const void* k, const void* v, int dtype,
+                                   const int64_t* qkv_strides, const uint8_t* mask,
+                                   const int64_t* mask_strides, void* out, int out_dtype,
+                                   int out_layout, int B, int H, int S, int head_dim,
+                                   int is_causal, double scale, int impl, int precision,
+                                   const int32_t* cu_seqlens, int64_t rows, int splits,
+                                   void* stream);
+
+/* Bytes of the per-GPU scratch array dotl_attention_forward_noalloc uses. */
+int64_t dotl_attention_noalloc_scratch_bytes(void);
+
+/*
  * The split count dotl_attention_forward would resolve `splits` (0, 1 or n)
  * to for these arguments, and the workspace bytes it then needs (0 when it
  * would not split). rows: B * S, or the packed row count. No device access.
