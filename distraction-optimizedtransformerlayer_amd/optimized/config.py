@@ -118,6 +118,10 @@ CUDA_GRAPH = "auto"
 # pins (the intermediates of one forward: ~1.5 GB at 41 M elements).
 _GRAPH_MAX_ACTIVATION = 1 << 26
 
+# "auto" keeps a graph only if its replay is at least this much faster than
+# the eager forward (a smaller gain is within the timing noise).
+_GRAPH_MIN_GAIN = 0.01
+
 # A captured pool larger than this share of the card is released.
 _GRAPH_POOL_SAFETY_FRACTION = 0.25
 

@@ -25,8 +25,8 @@ behind them is this build's:
   and writes the bound output -- and (3) no weight cache was rebuilt inside
   the capture (a cache built there would live in the graph's private pool).
 * Measured keep/decline. In "auto" a proven graph is then timed against the
-  eager forward on the same input (HIP events, median of three samples); it
-  is kept only if it is faster. "always" keeps every proven graph. Each
+  eager forward on the same input (HIP events, alternating samples, median
+  of five); it is kept only if it is at least config._GRAPH_MIN_GAIN faster. "always" keeps every proven graph. Each
   outcome and its timings go to `model._graph_log[key]`.
 * Failure isolation. An exception while capturing ends the capture (torch's
   context manager), then a one-element kernel checks the device still runs
@@ -90,7 +90,7 @@ class _GraphRunner:
 
     __slots__ = ("graph", "slot", "x_buf", "out_buf", "mask_buf", "maps_buf", "maps_src",
                  "in_bound", "out_bound", "out_shape", "out_dtype", "keepalive", "replays",
-                 "timing", "__weakref__")
+                 "timing", "bound_to", "__weakref__")
 
     def __init__(self) -> None:
         self.graph = None
@@ -107,6 +107,10 @@ class _GraphRunner:
         self.keepalive: Tuple = ()
         self.replays = 0
         self.timing: Dict[str, float] = {}
+        # (input address, output address, stream) the slot holds: a replay
+        # with the same three needs no bind (the caching allocator usually
+        # hands the output the block the previous one released)
+        self.bound_to: Optional[Tuple] = None
 
     def replay(self, x: torch.Tensor, mask: Optional[torch.Tensor],
                packing=None) -> torch.Tensor:
@@ -120,7 +124,12 @@ class _GraphRunner:
         out = (torch.empty(self.out_shape, dtype=self.out_dtype, device=x.device)
                if self.out_bound else None)
         if src is not None or out is not None:
-            kx.bind_io(self.slot, src, out)
+            stream = torch.cuda.current_stream(x.device)
+            want = (src.data_ptr() if src is not None else 0,
+                    out.data_ptr() if out is not None else 0, stream.cuda_stream)
+            if want != self.bound_to:
+                kx.bind_io(self.slot, src, out)
+                self.bound_to = want
         if self.mask_buf is not None:
             self.mask_buf.copy_(mask)
         if self.maps_buf is not None and packing is not self.maps_src:
@@ -202,20 +211,30 @@ def _weight_keepalive(model) -> Tuple:
     return tuple(held)
 
 
-def _time_calls(fn, n: int, samples: int = 3) -> float:
-    """Median device time (ms) of `n` back-to-back calls of `fn`."""
+def _time_calls(fn, n: int) -> float:
+    """Device time (ms) per call of `n` back-to-back calls of `fn`."""
     stream = torch.cuda.current_stream()
-    times = []
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(n):
+        fn()
+    stop.record(stream)
+    stop.synchronize()
+    return start.elapsed_time(stop) / n
+
+
+def _compare_timing(eager_call, replay_call, samples: int = 5) -> Tuple[float, float]:
+    """Median per-call device time (ms) of eager and replay, measured in
+    alternating samples of enough calls for ~10 ms each, so clock and
+    thermal drift hit both alike."""
+    single = max(_time_calls(eager_call, 1), 1e-3)
+    n = max(3, min(200, int(10.0 / single)))
+    eager, replay = [], []
     for _ in range(samples):
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(n):
-            fn()
-        stop.record(stream)
-        stop.synchronize()
-        times.append(start.elapsed_time(stop) / n)
-    return statistics.median(times)
+        eager.append(_time_calls(eager_call, n))
+        replay.append(_time_calls(replay_call, n))
+    return statistics.median(eager), statistics.median(replay)
 
 
 def _device_still_runs(device: torch.device) -> bool:
@@ -337,14 +356,11 @@ def _capture_graph(model, x: torch.Tensor, mask: Optional[torch.Tensor], use_mas
             if config.CUDA_GRAPH == "auto":
                 eager_call = lambda: model._forward_eager(x, mask, use_mask, packing)  # noqa: E731
                 replay_call = lambda: runner.replay(x, mask, packing)  # noqa: E731
-                single = _time_calls(eager_call, 1, 1)
-                n = max(2, min(50, int(2.0 / max(single, 1e-3))))
-                eager_ms = _time_calls(eager_call, n)
-                replay_ms = _time_calls(replay_call, n)
+                eager_ms, replay_ms = _compare_timing(eager_call, replay_call)
                 runner.replays = 0
                 runner.timing = {"eager_us": eager_ms * 1e3, "replay_us": replay_ms * 1e3}
                 log.update(runner.timing)
-                if replay_ms >= eager_ms:
+                if replay_ms > eager_ms * (1.0 - config._GRAPH_MIN_GAIN):
                     log["outcome"] = "declined: replay not faster than eager"
                     runner.release()
                     return None

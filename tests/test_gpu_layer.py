@@ -265,7 +265,8 @@ def test_graph_auto_keeps_only_a_faster_graph(kernels, name):
     (log,) = model._graph_log.values()
     print(f"[graph auto] {name}: {log}", flush=True)
     assert "eager_us" in log and "replay_us" in log
-    assert (log["outcome"] == "captured") == (log["replay_us"] < log["eager_us"])
+    kept = log["replay_us"] <= log["eager_us"] * (1.0 - ocfg._GRAPH_MIN_GAIN)
+    assert (log["outcome"] == "captured") == kept
     assert (len(model._graphs) == 1) == (log["outcome"] == "captured")
     for g in got:
         np.testing.assert_array_equal(g, eager)
