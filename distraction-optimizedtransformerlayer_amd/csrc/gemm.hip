@@ -39,7 +39,7 @@ namespace dotl {
 int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes);
 bool launch_gemm_dma(const _Float16* A, const _Float16* Alo, const _Float16* W,
                      const _Float16* Wlo, const float* bias, const float* R, void* C, int64_t M,
-                     int64_t N, int64_t K, int mode, int act, bool out_f16, int tile,
+                     int64_t N, int64_t K, int mode, int act, int out_dtype, int tile,
                      hipStream_t stream);
 
 namespace {
@@ -438,9 +438,16 @@ int linear_impl(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
                 int64_t N, int64_t K, int act, int math, int tile, void* stream) {
     clear_error();
     const char* who = act == DOTL_ACT_GELU ? "linear_gelu" : "linear_bias";
-    DOTL_REQUIRE(x_dtype == DOTL_F32 || x_dtype == DOTL_F16 || x_dtype == DOTL_F16X2,
-                 "%s: x must be float32, float16 or split float16", who);
-    DOTL_REQUIRE(out_dtype == DOTL_F32 || out_dtype == DOTL_F16, "%s: out must be float32 or float16", who);
+    DOTL_REQUIRE(x_dtype == DOTL_F32 || x_dtype == DOTL_F16 || x_dtype == DOTL_F16X2 ||
+                     x_dtype == DOTL_BF16,
+                 "%s: x must be float32, float16, bfloat16 or split float16", who);
+    DOTL_REQUIRE(out_dtype == DOTL_F32 || out_dtype == DOTL_F16 || out_dtype == DOTL_BF16,
+                 "%s: out must be float32, float16 or bfloat16", who);
+    DOTL_REQUIRE((x_dtype == DOTL_BF16) == (out_dtype == DOTL_BF16) || out_dtype == DOTL_F32,
+                 "%s: a bfloat16 x writes float32 or bfloat16, other x float32 or float16", who);
+    DOTL_REQUIRE(x_dtype != DOTL_BF16 || math == DOTL_MATH_FP16,
+                 "%s: a bfloat16 x (with a bfloat16 W) runs one pass (math %d)", who,
+                 DOTL_MATH_FP16);
     DOTL_REQUIRE(act == DOTL_ACT_NONE || act == DOTL_ACT_GELU, "%s: unknown activation %d", who, act);
     DOTL_REQUIRE(math == DOTL_MATH_FP16 || math == DOTL_MATH_FP16X3 || math == DOTL_MATH_FP16X2,
                  "%s: unknown math %d", who, math);
@@ -467,6 +474,7 @@ int linear_impl(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
     DOTL_REQUIRE(align % 16 == 0, "%s: x and W must be 16-byte aligned", who);
     const bool of16 = out_dtype == DOTL_F16;
     const bool split = math == DOTL_MATH_FP16X3;
+    const bool bf16 = x_dtype == DOTL_BF16;
 
     // LDS-DMA pipelined kernel: fp16 operands, K a multiple of 64, each
     // operand under 4 GiB (its per-lane DMA offsets are 32-bit).
@@ -476,13 +484,14 @@ int linear_impl(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
         const _Float16* xh = static_cast<const _Float16*>(x);
         const _Float16* xl = x_dtype == DOTL_F16X2 ? xh + M * K : nullptr;
         // split modes: bit 0 lo(W), bit 1 lo(x)
-        const int mode = math == DOTL_MATH_FP16X2 ? 2
-                         : (!split ? 0 : (x_dtype == DOTL_F16X2 ? 3 : 1));
+        const int mode = bf16 ? 4
+                         : (math == DOTL_MATH_FP16X2 ? 2
+                            : (!split ? 0 : (x_dtype == DOTL_F16X2 ? 3 : 1)));
         const int passes = 1 + (mode & 1) + ((mode >> 1) & 1);
         const int t = tile < 0 ? pick_dma_tile(M, N, K, passes) : tile;
         if (launch_gemm_dma(xh, xl, static_cast<const _Float16*>(w_hi),
                             static_cast<const _Float16*>(w_lo), bias, residual, out, M, N, K,
-                            mode, act, of16, t, as_stream(stream))) {
+                            mode, act, out_dtype, t, as_stream(stream))) {
             return check_launch(who);
         }
         DOTL_REQUIRE(x_dtype != DOTL_F16X2, "%s: tile id %d is not built for split passes", who, tile);
@@ -490,6 +499,11 @@ int linear_impl(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
     DOTL_REQUIRE(x_dtype != DOTL_F16X2,
                  "%s: split-fp16 x is served by the pipelined kernel only (K %% 64 == 0, operands "
                  "under 4 GiB)", who);
+    if (bf16) {
+        set_error(std::string(who) + ": bfloat16 operands are served by the pipelined kernel "
+                  "only (K % 64 == 0, operands under 4 GiB)");
+        return DOTL_DECLINED;
+    }
     if (residual != nullptr) {
         set_error(std::string(who) + ": the residual epilogue is served by the pipelined kernel "
                   "only (fp16 or split x, K % 64 == 0); add the residual separately");

@@ -21,9 +21,10 @@ struct DmaArgs {
     hipStream_t stream;
 };
 
-// Launches tile id `tile` for MODE (bit 0 split W, bit 1 split x), ACT and
-// the output type; false when that tile is not built for the mode.
-template <int MODE, int ACT, bool OUT_F16>
+// Launches tile id `tile` for MODE (bit 0 split W, bit 1 split x; 4 bf16
+// operands), ACT and the output dtype code (DOTL_F32, DOTL_F16 for modes
+// 0-3, DOTL_BF16 for mode 4); false when that tile is not built for the mode.
+template <int MODE, int ACT, int OUTT>
 bool dispatch_tile(const DmaArgs& a, int tile);
 
 }  // namespace gemm_dma

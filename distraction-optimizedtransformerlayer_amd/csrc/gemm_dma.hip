@@ -35,23 +35,27 @@ int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
 
 bool launch_gemm_dma(const _Float16* A, const _Float16* Alo, const _Float16* W,
                      const _Float16* Wlo, const float* bias, const float* R, void* C, int64_t M,
-                     int64_t N, int64_t K, int mode, int act, bool out_f16, int tile,
+                     int64_t N, int64_t K, int mode, int act, int out_dtype, int tile,
                      hipStream_t stream) {
     const DmaArgs a{A, Alo, W, Wlo, bias, R, C, M, N, K, stream};
     auto by_out = [&](auto m) {
         constexpr int MD = decltype(m)::value;
+        constexpr int O16 = MD == 4 ? DOTL_BF16 : DOTL_F16;
+        if (out_dtype != DOTL_F32 && out_dtype != O16) return false;
+        const bool o32 = out_dtype == DOTL_F32;
         if (act == DOTL_ACT_GELU) {
-            return out_f16 ? dispatch_tile<MD, DOTL_ACT_GELU, true>(a, tile)
-                           : dispatch_tile<MD, DOTL_ACT_GELU, false>(a, tile);
+            return o32 ? dispatch_tile<MD, DOTL_ACT_GELU, DOTL_F32>(a, tile)
+                       : dispatch_tile<MD, DOTL_ACT_GELU, O16>(a, tile);
         }
-        return out_f16 ? dispatch_tile<MD, DOTL_ACT_NONE, true>(a, tile)
-                       : dispatch_tile<MD, DOTL_ACT_NONE, false>(a, tile);
+        return o32 ? dispatch_tile<MD, DOTL_ACT_NONE, DOTL_F32>(a, tile)
+                   : dispatch_tile<MD, DOTL_ACT_NONE, O16>(a, tile);
     };
     switch (mode) {
         case 0: return by_out(std::integral_constant<int, 0>{});
         case 1: return by_out(std::integral_constant<int, 1>{});
         case 2: return by_out(std::integral_constant<int, 2>{});
         case 3: return by_out(std::integral_constant<int, 3>{});
+        case 4: return by_out(std::integral_constant<int, 4>{});
     }
     return false;
 }

@@ -32,6 +32,7 @@
 //   * rows past M (or N) are clamped to the last valid row -- those outputs
 //     are never stored -- so every DMA is in bounds and branch-free; K must
 //     be a multiple of 64 (no K tail);
+//   * MODE 4 streams bf16 x and W (v_mfma_f32_32x32x16_bf16), one pass;
 //   * MODE (bit 0: split W, bit 1: split x) sets the passes: 0 x*W; 1
 //     x*W + 2^-12 x*lo(W) (x exact in fp16); 2 hi(x)*W + 2^-12 lo(x)*W (x
 //     given as fp16 hi/lo planes, W in fp16); 3 all three products: the
@@ -43,6 +44,8 @@
 //     from one row address per tile. The epilogue's cost matters here: with
 //     one workgroup per CU nothing overlaps it, and at the configs' short K
 //     (256-512) it was costing more than the MFMAs.
+#include <type_traits>
+
 #include "dotl_dma.h"
 #include "gemm_dma.h"
 
@@ -90,10 +93,12 @@ struct DmaLayout {
     __device__ __forceinline__ static int swz(int row) { return (row / SWZ_DIV) % CPR; }
 };
 
-template <int BM, int BN, int BK, int NS, int MODE, int ACT, bool OUT_F16>
+template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT>
 struct DmaGemm {
     using L = DmaLayout<BM, BN, BK, MODE>;
-    static constexpr bool SPLIT = MODE != 0;
+    static constexpr bool SPLIT = (MODE & 3) != 0;
+    // MODE 4: bf16 operands (the LDS stages hold 16-bit values either way), one pass
+    static constexpr bool BF16 = MODE == 4;
     static constexpr int WM = BM / 2, WN = BN / 2;
     static constexpr int TM = WM / 32, TN = WN / 32;
 
@@ -156,6 +161,17 @@ struct DmaGemm {
         static_for<LO, HI>([&](auto dd) { issue_one<decltype(dd)::value>(stage, kt); });
     }
 
+    // One 32x32x16 product on the operand type the mode streams.
+    __device__ __forceinline__ static floatx16 mma(half8 b, half8 a, floatx16 c) {
+        if constexpr (BF16) {
+            return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, b),
+                                                           __builtin_bit_cast(bf16x8, a), c, 0,
+                                                           0, 0);
+        } else {
+            return __builtin_amdgcn_mfma_f32_32x32x16_f16(b, a, c, 0, 0, 0);
+        }
+    }
+
     // Fragment of row `row` (tile-local), 16-wide k step `ks`: the 8 halves of
     // lane group lg, at the swizzled chunk.
     __device__ __forceinline__ half8 frag(const _Float16* region, int row, int ks) const {
@@ -181,7 +197,7 @@ struct DmaGemm {
                 constexpr int i = decltype(ii)::value;
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], a[i], acc[i][j], 0, 0, 0);
+                    acc[i][j] = mma(b[j], a[i], acc[i][j]);
                 constexpr int slot = ks * TM + i;
                 if (more) issue_range<slot * NDMA / SLOTS, (slot + 1) * NDMA / SLOTS>(next, kt_next);
             });
@@ -224,13 +240,13 @@ struct DmaGemm {
     }
 };
 
-template <int BM, int BN, int BK, int NS, int MODE, int ACT, bool OUT_F16>
+template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT>
 __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     const _Float16* __restrict__ A, const _Float16* __restrict__ Alo,
     const _Float16* __restrict__ W, const _Float16* __restrict__ Wlo,
     const float* __restrict__ bias, const float* __restrict__ R, void* __restrict__ C, int64_t M,
     int64_t N, int64_t K) {
-    using G = DmaGemm<BM, BN, BK, NS, MODE, ACT, OUT_F16>;
+    using G = DmaGemm<BM, BN, BK, NS, MODE, ACT, OUTT>;
     using L = typename G::L;
     static_assert(NS >= 2 && NS <= 8, "2 to 8 stages");
     static_assert((NS - 2) * L::LOADS < 64, "vmcnt is 6 bits");
@@ -349,8 +365,6 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     for (int i = 0; i < G::TM; ++i) {
         const int64_t row = g.m0 + g.wm * G::WM + i * 32 + g.lr;
         if (row >= M) continue;
-        float* crow32 = static_cast<float*>(C) + row * N;
-        _Float16* crow16 = static_cast<_Float16*>(C) + row * N;
 #pragma unroll
         for (int j = 0; j < G::TN; ++j) {
 #pragma unroll
@@ -366,7 +380,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
                     if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
                     v[e] = a;
                 }
-                if constexpr (!OUT_F16) {
+                if constexpr (OUTT == DOTL_F32) {
                     // residual stream: out = R + act(x W^T + b), the add the
                     // following LayerNorm would otherwise do (same fp32 sum)
                     if (R != nullptr) {
@@ -382,107 +396,100 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
                         }
                     }
                 }
+                using TO = typename std::conditional<
+                    OUTT == DOTL_F32, float,
+                    typename std::conditional<OUTT == DOTL_BF16, __bf16, _Float16>::type>::type;
+                TO* crow = static_cast<TO*>(C) + row * N;
                 if (vec_ok && col + 4 <= N) {
-                    if constexpr (OUT_F16) {
-                        half4 h;
-                        h[0] = to_half(v[0]); h[1] = to_half(v[1]);
-                        h[2] = to_half(v[2]); h[3] = to_half(v[3]);
-                        *reinterpret_cast<half4*>(crow16 + col) = h;
-                    } else {
-                        *reinterpret_cast<float4*>(crow32 + col) = make_float4(v[0], v[1], v[2], v[3]);
-                    }
+                    store4f(crow + col, make_float4(v[0], v[1], v[2], v[3]));
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        if (col + e < N) {
-                            if constexpr (OUT_F16) crow16[col + e] = to_half(v[e]);
-                            else crow32[col + e] = v[e];
-                        }
-                    }
+                    for (int e = 0; e < 4; ++e)
+                        if (col + e < N) crow[col + e] = from_f32<TO>(v[e]);
                 }
             }
         }
     }
 }
 
-template <int BM, int BN, int BK, int NS, int MODE, int ACT, bool OUT_F16>
+template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT>
 void launch_dma(const DmaArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, MODE, ACT, OUT_F16>),
+    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, MODE, ACT, OUTT>),
                        dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, a.stream, a.A,
                        a.Alo, a.W, a.Wlo, a.bias, a.R, a.C, a.M, a.N, a.K);
 }
 
 // Tile ids (dotl_linear's `tile`): 0 128x128, 1 256x128, 2 64x64, 3 256x256,
 // 4 128x64. K tiles of 32; stage counts fill <= 144 KiB of LDS.
-template <int MODE, int ACT, bool OUT_F16>
+template <int MODE, int ACT, int OUTT>
 bool dispatch_tile(const DmaArgs& a, int tile) {
     // Stage depths are chosen by operand planes a stage holds: 2 + split ones.
     constexpr int PASSES = 1 + (MODE & 1) + ((MODE >> 1) & 1);
     switch (tile) {
         case 0:   // stage: 256 / 384 / 512 rows x 64 B = 16 / 24 / 32 KiB
-            if constexpr (PASSES == 1) launch_dma<128, 128, 32, 8, MODE, ACT, OUT_F16>(a);
-            else if constexpr (PASSES == 2) launch_dma<128, 128, 32, 6, MODE, ACT, OUT_F16>(a);
-            else launch_dma<128, 128, 32, 4, MODE, ACT, OUT_F16>(a);
+            if constexpr (PASSES == 1) launch_dma<128, 128, 32, 8, MODE, ACT, OUTT>(a);
+            else if constexpr (PASSES == 2) launch_dma<128, 128, 32, 6, MODE, ACT, OUTT>(a);
+            else launch_dma<128, 128, 32, 4, MODE, ACT, OUTT>(a);
             return true;
         case 1:   // 384 rows: 24 KiB
-            if constexpr (PASSES == 1) { launch_dma<256, 128, 32, 6, MODE, ACT, OUT_F16>(a); return true; }
+            if constexpr (PASSES == 1) { launch_dma<256, 128, 32, 6, MODE, ACT, OUTT>(a); return true; }
             return false;
         case 2:   // 128 / 192 / 256 rows
-            if constexpr (PASSES == 1) launch_dma<64, 64, 32, 8, MODE, ACT, OUT_F16>(a);
-            else launch_dma<64, 64, 32, 8, MODE, ACT, OUT_F16>(a);
+            if constexpr (PASSES == 1) launch_dma<64, 64, 32, 8, MODE, ACT, OUTT>(a);
+            else launch_dma<64, 64, 32, 8, MODE, ACT, OUTT>(a);
             return true;
         case 3:   // 512 rows: 32 KiB
-            if constexpr (PASSES == 1) { launch_dma<256, 256, 32, 4, MODE, ACT, OUT_F16>(a); return true; }
+            if constexpr (PASSES == 1) { launch_dma<256, 256, 32, 4, MODE, ACT, OUTT>(a); return true; }
             return false;
         case 4:   // 192 / 320 / 384 rows
-            if constexpr (PASSES == 1) launch_dma<128, 64, 32, 8, MODE, ACT, OUT_F16>(a);
-            else if constexpr (PASSES == 2) launch_dma<128, 64, 32, 7, MODE, ACT, OUT_F16>(a);
-            else launch_dma<128, 64, 32, 6, MODE, ACT, OUT_F16>(a);
+            if constexpr (PASSES == 1) launch_dma<128, 64, 32, 8, MODE, ACT, OUTT>(a);
+            else if constexpr (PASSES == 2) launch_dma<128, 64, 32, 7, MODE, ACT, OUTT>(a);
+            else launch_dma<128, 64, 32, 6, MODE, ACT, OUTT>(a);
             return true;
         // Shallow pipelines whose LDS (<= 72 KiB) lets two workgroups share a
         // CU, i.e. two waves per SIMD, the co-resident one hiding latency.
         case 5:
-            if constexpr (PASSES == 1) launch_dma<128, 128, 32, 4, MODE, ACT, OUT_F16>(a);
-            else if constexpr (PASSES == 2) launch_dma<128, 128, 32, 3, MODE, ACT, OUT_F16>(a);
-            else launch_dma<128, 128, 32, 2, MODE, ACT, OUT_F16>(a);
+            if constexpr (PASSES == 1) launch_dma<128, 128, 32, 4, MODE, ACT, OUTT>(a);
+            else if constexpr (PASSES == 2) launch_dma<128, 128, 32, 3, MODE, ACT, OUTT>(a);
+            else launch_dma<128, 128, 32, 2, MODE, ACT, OUTT>(a);
             return true;
         case 6:
-            if constexpr (PASSES == 1) { launch_dma<256, 128, 32, 3, MODE, ACT, OUT_F16>(a); return true; }
+            if constexpr (PASSES == 1) { launch_dma<256, 128, 32, 3, MODE, ACT, OUTT>(a); return true; }
             return false;
         case 7:
-            if constexpr (PASSES == 1) launch_dma<128, 64, 32, 4, MODE, ACT, OUT_F16>(a);
-            else launch_dma<128, 64, 32, 3, MODE, ACT, OUT_F16>(a);
+            if constexpr (PASSES == 1) launch_dma<128, 64, 32, 4, MODE, ACT, OUTT>(a);
+            else launch_dma<128, 64, 32, 3, MODE, ACT, OUTT>(a);
             return true;
         case 8:
-            launch_dma<64, 64, 32, 4, MODE, ACT, OUT_F16>(a);
+            launch_dma<64, 64, 32, 4, MODE, ACT, OUTT>(a);
             return true;
         // BK = 64: each row of a stage is one whole 128-byte line, so every
         // DMA instruction reads 8 full lines instead of 16 half lines.
         case 9:   // 512 rows x 128 B = 64 KiB a stage
-            if constexpr (PASSES == 1) { launch_dma<256, 256, 64, 2, MODE, ACT, OUT_F16>(a); return true; }
+            if constexpr (PASSES == 1) { launch_dma<256, 256, 64, 2, MODE, ACT, OUTT>(a); return true; }
             return false;
         case 10:  // 256 / 384 / 512 rows: 32 / 48 / 64 KiB
-            if constexpr (PASSES == 1) launch_dma<128, 128, 64, 4, MODE, ACT, OUT_F16>(a);
-            else if constexpr (PASSES == 2) launch_dma<128, 128, 64, 3, MODE, ACT, OUT_F16>(a);
-            else launch_dma<128, 128, 64, 2, MODE, ACT, OUT_F16>(a);
+            if constexpr (PASSES == 1) launch_dma<128, 128, 64, 4, MODE, ACT, OUTT>(a);
+            else if constexpr (PASSES == 2) launch_dma<128, 128, 64, 3, MODE, ACT, OUTT>(a);
+            else launch_dma<128, 128, 64, 2, MODE, ACT, OUTT>(a);
             return true;
         case 11:  // 384 rows: 48 KiB
-            if constexpr (PASSES == 1) { launch_dma<256, 128, 64, 3, MODE, ACT, OUT_F16>(a); return true; }
+            if constexpr (PASSES == 1) { launch_dma<256, 128, 64, 3, MODE, ACT, OUTT>(a); return true; }
             return false;
         case 12:  // two workgroups a CU
-            if constexpr (PASSES == 1) { launch_dma<128, 128, 64, 2, MODE, ACT, OUT_F16>(a); return true; }
+            if constexpr (PASSES == 1) { launch_dma<128, 128, 64, 2, MODE, ACT, OUTT>(a); return true; }
             return false;
         case 13:  // 192 / 320 / 384 rows
-            if constexpr (PASSES == 1) launch_dma<128, 64, 64, 3, MODE, ACT, OUT_F16>(a);
-            else launch_dma<128, 64, 64, 2, MODE, ACT, OUT_F16>(a);
+            if constexpr (PASSES == 1) launch_dma<128, 64, 64, 3, MODE, ACT, OUTT>(a);
+            else launch_dma<128, 64, 64, 2, MODE, ACT, OUTT>(a);
             return true;
         // 192x128: fewer, larger tiles where 128-row tiles leave a short
         // second wave of workgroups. 320 / 512 rows: 40 / 64 KiB a stage
         // (three passes would not fit two stages).
         case 14:
-            if constexpr (PASSES == 1) { launch_dma<192, 128, 64, 3, MODE, ACT, OUT_F16>(a); return true; }
-            else if constexpr (PASSES == 2) { launch_dma<192, 128, 64, 2, MODE, ACT, OUT_F16>(a); return true; }
+            if constexpr (PASSES == 1) { launch_dma<192, 128, 64, 3, MODE, ACT, OUTT>(a); return true; }
+            else if constexpr (PASSES == 2) { launch_dma<192, 128, 64, 2, MODE, ACT, OUTT>(a); return true; }
             return false;
     }
     return false;
@@ -491,12 +498,16 @@ bool dispatch_tile(const DmaArgs& a, int tile) {
 }  // namespace gemm_dma
 }  // namespace dotl
 
+// One mode's instances: fp32 output and the mode's 16-bit output (fp16 for
+// the fp16 modes 0-3, bf16 for mode 4), with and without GELU.
 #define DOTL_GEMM_DMA_INSTANTIATE(M)                                                            \
     namespace dotl {                                                                            \
     namespace gemm_dma {                                                                        \
-    template bool dispatch_tile<M, DOTL_ACT_NONE, false>(const DmaArgs&, int);                  \
-    template bool dispatch_tile<M, DOTL_ACT_NONE, true>(const DmaArgs&, int);                   \
-    template bool dispatch_tile<M, DOTL_ACT_GELU, false>(const DmaArgs&, int);                  \
-    template bool dispatch_tile<M, DOTL_ACT_GELU, true>(const DmaArgs&, int);                   \
+    template bool dispatch_tile<M, DOTL_ACT_NONE, DOTL_F32>(const DmaArgs&, int);               \
+    template bool dispatch_tile<M, DOTL_ACT_NONE, (M == 4 ? DOTL_BF16 : DOTL_F16)>(             \
+        const DmaArgs&, int);                                                                   \
+    template bool dispatch_tile<M, DOTL_ACT_GELU, DOTL_F32>(const DmaArgs&, int);               \
+    template bool dispatch_tile<M, DOTL_ACT_GELU, (M == 4 ? DOTL_BF16 : DOTL_F16)>(             \
+        const DmaArgs&, int);                                                                   \
     }                                                                                           \
     }

@@ -446,7 +446,7 @@ class Kernels:
         return self._wcache_builds
 
     def weight_cache_tensors(self) -> List[object]:
-        """Every live cached fp16 weight buffer (graph capture pins these)."""
+        """Every live cached weight (and 16-bit bias) copy (graph capture pins these)."""
         out = []
         for ref, _, hi, lo in self._wcache.values():
             if ref() is not None:
@@ -467,11 +467,14 @@ class Kernels:
         if bias.numel() != weight.shape[0]:
             raise RuntimeError(f"{who}: bias must have {weight.shape[0]} elements")
         xcode = _dtype_code(x)
-        if (xcode is None or weight.dtype != torch.float32 or bias.dtype != torch.float32):
-            return None  # declined: the caller falls back
         K, N = weight.shape[1], weight.shape[0]
         if K % 8 != 0 or K == 0:
             return None
+        if weight.dtype in (torch.float16, torch.bfloat16):
+            return self._gemm16(who, x, weight, bias, tile, act, residual)
+        if (xcode not in (DOTL_F32, DOTL_F16) or weight.dtype != torch.float32
+                or bias.dtype != torch.float32):
+            return None  # declined: the caller falls back
         # math: -1 auto -> fp16 operands; 0 (the reference's tf32 slot) -> the
         # split fp16x3 path, which needs an fp32 x.
         m = DOTL_MATH_FP16 if math in (-1, None) else DOTL_MATH_FP16X3
@@ -495,6 +498,42 @@ class Kernels:
                 xc.data_ptr(), xcode, hi.data_ptr(), lo.data_ptr() if lo is not None else None,
                 bc.data_ptr(), out.data_ptr(), DOTL_F16 if out_half else DOTL_F32, M, N, K, act,
                 m, int(tile), self._stream(x.device)))
+        if rc == DOTL_DECLINED:
+            return None
+        return out
+
+    def bias_f32(self, bias):
+        """An fp32 copy of a 16-bit bias (the epilogue adds in fp32), cached
+        per tensor and version like the weight copies."""
+        import torch
+
+        key = (bias.data_ptr(), bias.numel(), str(bias.device), _version_or_none(bias))
+        ent = self._wcache.get(("bias", id(bias)))
+        if ent is not None and ent[0]() is bias and ent[1] == key:
+            return ent[2]
+        b32 = bias.detach().to(torch.float32).contiguous()
+        self._wcache[("bias", id(bias))] = (weakref.ref(bias), key, b32, None)
+        self._wcache_builds += 1
+        return b32
+
+    def _gemm16(self, who, x, weight, bias, tile, act, residual):
+        """A 16-bit model's projection: x, W (as it is) and the output in the
+        weight's dtype, one MFMA pass (fp16 or bf16 operands), fp32
+        accumulation, bias and GELU. The residual epilogue is fp32-only:
+        with one the call declines and the caller adds it."""
+        import torch
+
+        if x.dtype != weight.dtype or residual is not None:
+            return None
+        code = DOTL_F16 if weight.dtype == torch.float16 else DOTL_BF16
+        K, N = weight.shape[1], weight.shape[0]
+        xc, wc = x.contiguous(), weight.detach().contiguous()
+        M = xc.numel() // K
+        b32 = self.bias_f32(bias)
+        out = torch.empty((*xc.shape[:-1], N), dtype=weight.dtype, device=xc.device)
+        rc = self._check(self._lib.dotl_linear(
+            xc.data_ptr(), code, wc.data_ptr(), None, b32.data_ptr(), out.data_ptr(), code, M, N,
+            K, act, DOTL_MATH_FP16, int(tile), self._stream(x.device)))
         if rc == DOTL_DECLINED:
             return None
         return out

@@ -107,7 +107,9 @@ def _custom_kernels():
 
 def _add_layernorm(x: torch.Tensor, sub: torch.Tensor, norm,
                    normed_half: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
-    """(x + sub, norm(x + sub)) in one kernel."""
+    """(x + sub, norm(x + sub)) in one kernel. A 16-bit x keeps its dtype
+    throughout (normed_half narrows fp32 only)."""
+    normed_half = normed_half and x.dtype == torch.float32
     kernels = _custom_kernels()
     if kernels is not None:
         return tuple(kernels.fused_add_layernorm(x, sub, norm.weight, norm.bias, norm.eps,
@@ -143,7 +145,9 @@ def _entry_norm(x: torch.Tensor, norm) -> Tuple[torch.Tensor, torch.Tensor]:
     if io is None:
         return x, norm(x)
     rows, width = x.numel() // x.shape[-1], x.shape[-1]
-    if _normed_split_wanted():
+    if x.dtype != torch.float32:
+        kind = "float"     # the normed output in x's own dtype
+    elif _normed_split_wanted():
         kind = "split"
     elif _normed_wants_fp16(rows, width):
         kind = "half"
@@ -165,7 +169,7 @@ def _linear_gelu(x: torch.Tensor, lin, out_half: bool = False) -> torch.Tensor:
                 return out
     fallback_counts["linear_gelu"] += 1
     out = F.gelu(F.linear(x.to(lin.weight.dtype), lin.weight, lin.bias), approximate="none")
-    return out.half() if out_half else out
+    return out.half() if (out_half and out.dtype == torch.float32) else out
 
 
 def _split_planes(t: torch.Tensor) -> torch.Tensor:
@@ -188,7 +192,10 @@ def _normed_split_wanted() -> bool:
 
 
 def _layernorm_split(x: torch.Tensor, norm) -> torch.Tensor:
-    """LayerNorm(x) as split fp16 planes [2, *x.shape]."""
+    """LayerNorm(x) as split fp16 planes [2, *x.shape]; for a 16-bit x, the
+    plain LayerNorm in x's dtype (planes carry fp32 values only)."""
+    if x.dtype != torch.float32:
+        return _layernorm(x, norm)
     kernels = _custom_kernels()
     if kernels is not None:
         return kernels.fused_layernorm_split(x, norm.weight, norm.bias, norm.eps)
@@ -197,7 +204,10 @@ def _layernorm_split(x: torch.Tensor, norm) -> torch.Tensor:
 
 
 def _add_layernorm_split(x: torch.Tensor, sub: torch.Tensor, norm):
-    """(x + sub, LayerNorm(x + sub) as split fp16 planes)."""
+    """(x + sub, LayerNorm(x + sub) as split fp16 planes); a 16-bit x gets
+    the plain add+LayerNorm in its dtype."""
+    if x.dtype != torch.float32:
+        return _add_layernorm(x, sub, norm)
     kernels = _custom_kernels()
     if kernels is not None:
         return tuple(kernels.fused_add_layernorm_split(x, sub, norm.weight, norm.bias, norm.eps))
@@ -230,7 +240,9 @@ def _layernorm_pack(x: torch.Tensor, norm, packing) -> Tuple[torch.Tensor, torch
     decides.
     """
     width = x.shape[-1]
-    if _normed_split_wanted():
+    if x.dtype != torch.float32:
+        kind = "float"     # the normed rows in x's own dtype
+    elif _normed_split_wanted():
         kind = "split"
     elif _normed_wants_fp16(packing.t_valid, width):
         kind = "half"
@@ -295,6 +307,7 @@ def _layernorm(x: torch.Tensor, norm, out_half: bool = False,
 
     `output`: this is the forward's output norm (bound to the graph's I/O
     slot while capturing)."""
+    out_half = out_half and x.dtype == torch.float32
     if config.LAYERNORM != "off":
         kernels = _custom_kernels()
         if kernels is not None:
@@ -380,7 +393,10 @@ def _linear_bias(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Ten
     out = F.linear(x.to(weight.dtype), weight, bias)
     if residual is not None:
         out = residual + out
-    want = torch.float16 if out_half else torch.float32
+    if x.dtype in (torch.float16, torch.bfloat16):
+        want = x.dtype
+    else:
+        want = torch.float16 if out_half else torch.float32
     return out if out.dtype == want else out.to(want)
 
 

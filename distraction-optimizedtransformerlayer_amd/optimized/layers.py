@@ -234,7 +234,8 @@ class MyTransformerBlock(nn.Module):
         rows = x.numel() // d_model
         # the epilogue is the pipelined kernel's: fp16 operands in (ctx from
         # attention, hidden from linear_gelu), K a multiple of 64
-        return (_residual_epilogue_wanted(d_model) and _residual_epilogue_wanted(d_ff)
+        return (x.dtype == torch.float32
+                and _residual_epilogue_wanted(d_model) and _residual_epilogue_wanted(d_ff)
                 and _attention_wants_fp16() and _gelu_output_wants_fp16(rows)
                 and not _ffn_block_eligible(x, self.ffn_in, self.ffn_out))
 

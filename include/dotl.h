@@ -148,11 +148,16 @@ int dotl_weight_split(const float* w, void* w_hi, void* w_lo, int64_t n, void* s
  * Replaces linear_bias / linear_gelu (reference csrc/linear_gelu.cuh:598-756).
  *
  *   x         [M, K] contiguous, x_dtype DOTL_F32 (narrowed with RNE when
- *             staged), DOTL_F16, or DOTL_F16X2 ([2][M][K] hi/lo planes)
- *   w_hi      [N, K] fp16 from dotl_weight_split
+ *             staged), DOTL_F16, DOTL_F16X2 ([2][M][K] hi/lo planes), or
+ *             DOTL_BF16 (with a bf16 W, one pass on v_mfma_f32_32x32x16_bf16,
+ *             K % 64 == 0; the reference's BFloat16 dispatch,
+ *             csrc/linear_gelu.cuh:598-719): a 16-bit model's own weights
+ *   w_hi      [N, K] fp16 from dotl_weight_split (or a model's fp16 weight as
+ *             it is), bf16 for a DOTL_BF16 x
  *   w_lo      [N, K] fp16 scaled residual; required for DOTL_MATH_FP16X3
  *   bias      [N] float32 (required; the reference's kernels always add one)
- *   out       [M, N], out_dtype DOTL_F32 or DOTL_F16 (RNE)
+ *   out       [M, N], out_dtype DOTL_F32, DOTL_F16 (RNE; not with a bf16 x) or
+ *             DOTL_BF16 (RNE; bf16 x only)
  *   act       DOTL_ACT_NONE / DOTL_ACT_GELU, applied in fp32 before the store
  *   math      DOTL_MATH_FP16, DOTL_MATH_FP16X3 (an fp16 x is exact in
  *             fp16, so with it the split path runs two passes: x*hi + x*lo;

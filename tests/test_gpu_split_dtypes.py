@@ -187,3 +187,42 @@ def test_attention_bf16_tensors(kernels, B, H, S, hd, causal, padded):
     exact = kernels.fused_attention_forward(qb, kb, vb, mask, causal, scale, 1, 0, 0)
     assert exact.dtype == torch.bfloat16
     np.testing.assert_allclose(exact.double().cpu().numpy(), want, atol=4e-3, rtol=2 ** -7)
+
+
+# ---- 16-bit tensors: GEMMs -------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K", [(300, 512, 256), (4096, 1536, 512), (77, 128, 1024)])
+@pytest.mark.parametrize("act", ["none", "gelu"])
+def test_gemm_16bit_tensors(kernels, dtype, M, N, K, act):
+    """A 16-bit model's projection: x, W, bias and the output in the model
+    dtype, one pass of fp16 / bf16 MFMAs with fp32 accumulation. Against fp64
+    on the same 16-bit operands, within the output's own rounding (2^-11
+    relative for fp16, 2^-8 for bf16) plus accumulation order (2e-4 |.|)."""
+    r = np.random.default_rng(M + N + K)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    w = (r.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32)
+    b = (0.1 * r.standard_normal(N)).astype(np.float32)
+    xt, wt, bt = (_t(a).to(dtype) for a in (x, w, b))
+    fn = kernels.linear_gelu if act == "gelu" else kernels.linear_bias
+    out = fn(xt, wt, bt)
+    assert out is not None and out.dtype == dtype
+    ref = _round(x, dtype) @ _round(w, dtype).T + _round(b, dtype)
+    if act == "gelu":
+        ref = brute.gelu(ref)
+    ulp = 2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7
+    np.testing.assert_allclose(out.double().cpu().numpy(), ref, rtol=ulp, atol=ulp)
+
+
+def test_gemm_16bit_declines_what_it_does_not_cover(kernels):
+    x = torch.randn(64, 96, device=DEV).bfloat16()          # K % 64 != 0 for bf16
+    w = torch.randn(32, 96, device=DEV).bfloat16()
+    b = torch.zeros(32, device=DEV).bfloat16()
+    assert kernels.linear_bias(x, w, b) is None
+    # a residual epilogue is fp32-only
+    x = torch.randn(64, 128, device=DEV).half()
+    w = torch.randn(32, 128, device=DEV).half()
+    b = torch.zeros(32, device=DEV).half()
+    assert kernels.linear_bias(x, w, b, residual=torch.zeros(64, 32, device=DEV)) is None
+    # mixed dtypes are not a 16-bit model's projection
+    assert kernels.linear_bias(x.bfloat16(), w, b) is None
