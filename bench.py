@@ -176,20 +176,38 @@ def layer_ops(cfg, model, x, mask):
     scale = hd ** -0.5
     fw, fb = model.final_norm.weight, model.final_norm.bias
 
+    from optimized import kernels as okernels
+
+    # The QKV arithmetic the model resolves for this input (config.QKV_PRECISION
+    # "auto": split planes where some row attends to few keys, else one pass).
+    okernels._qkv_few_keys = model._few_key_rows(x, model._mask_packing(mask))
+    qkv_prec = okernels._qkv_precision()
+    split = qkv_prec in ("fp16x2", "fp16x3")
+    split_w = qkv_prec == "fp16x3"
+    kind = "split" if split else "half"
     with torch.inference_mode():
         if packing is not None:
             ln1 = lambda: kx.fused_layernorm_rows(x, layer.norm1.weight, layer.norm1.bias,  # noqa: E731
-                                                  packing.idx, 1e-5, "split", True)
+                                                  packing.idx, 1e-5, kind, True)
             x2, planes = ln1()
-            ln1_bytes = R * D * 12.0            # read x, write the gathered x and the planes
+            # read x, write the gathered x and the planes (or fp16 normed)
+            ln1_bytes = R * D * (12.0 if split else 10.0)
         else:
             x2 = x.reshape(T, D)
-            ln1 = lambda: kx.fused_layernorm_split(x2, layer.norm1.weight, layer.norm1.bias)  # noqa: E731
+            if split:
+                ln1 = lambda: kx.fused_layernorm_split(x2, layer.norm1.weight, layer.norm1.bias)  # noqa: E731
+            else:
+                ln1 = lambda: kx.fused_layernorm(x2, layer.norm1.weight, layer.norm1.bias, 1e-5,  # noqa: E731
+                                                 True)
             planes = ln1()
-            ln1_bytes = T * D * 8.0
+            ln1_bytes = T * D * (8.0 if split else 6.0)
         qkv_w, qkv_b = attn._get_qkv_weight()
-        split_w = ocfg.QKV_PRECISION == "fp16x3"
-        qkv = kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True, split_weight=split_w)
+        if split:
+            qkv_fn = lambda: kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True,  # noqa: E731
+                                                  split_weight=split_w)
+        else:
+            qkv_fn = lambda: kx.linear_bias(planes, qkv_w, qkv_b, -1, -1, True)  # noqa: E731
+        qkv = qkv_fn()
         if packing is not None:
             q, k, v = qkv.view(R, 3, H, hd).unbind(1)
             attn_fn = lambda: kx.fused_attention_forward(q, k, v, None, cfg.causal, scale, 0, 1, 0,  # noqa: E731
@@ -239,10 +257,10 @@ def layer_ops(cfg, model, x, mask):
     w16 = lambda lin: 2.0 * lin.weight.numel() + nb(lin.bias)  # noqa: E731
     cu_bytes = nb(packing.cu) if packing is not None else nb(mask)
     ops = {
-        "layernorm (norm1, split-fp16 out)": (ln1, "hbm", ln1_bytes, ln1_bytes),
-        f"linear qkv ({ocfg.QKV_PRECISION}, fp16 out)": (
-            lambda: kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True, split_weight=split_w),
-            "mfma", 2.0 * R * D * 3 * D, nb(planes, qkv_b, qkv) + wq16),
+        f"layernorm (norm1, {'split-fp16' if split else 'fp16'} out)": (
+            ln1, "hbm", ln1_bytes, ln1_bytes),
+        f"linear qkv ({qkv_prec}, fp16 out)": (
+            qkv_fn, "mfma", 2.0 * R * D * 3 * D, nb(planes, qkv_b, qkv) + wq16),
         "attention": (attn_fn, "mfma", attention_useful_flops(cfg, L), nb(qkv, ctx) + cu_bytes),
         "linear out_proj" + (" (+ residual)" if resid else ""): (
             lambda: kx.linear_bias(ctx2, attn.out_proj.weight, attn.out_proj.bias,
@@ -569,10 +587,10 @@ def _main(out):
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("fp32 I/O; fp16 MFMA operands, fp32 accumulate (QKV: "
-                  + {"fp16x2": "LayerNorm output as split fp16 hi+lo, two passes",
-                     "fp16x3": "split fp16x3, three passes",
-                     "fp16": "one fp16 pass"}[ocfg.QKV_PRECISION] + ")"),
+        "dtype": ("fp32 I/O; fp16 MFMA operands, fp32 accumulate (QKV "
+                  + ocfg.QKV_PRECISION + ": LayerNorm output as split fp16 hi+lo, two "
+                  "passes, where some query row attends to < "
+                  + str(ocfg._QKV_SPLIT_MIN_KEYS) + " keys; else one fp16 pass)"),
         "data": "synthetic (seeded Xavier weights, N(0,1) x, key-padding lengths)",
         "config": {"workload": f"{cfg.name}: single-layer forward B={cfg.batch_size} "
                                f"S={cfg.seq_len} d_model={cfg.d_model} heads={cfg.num_heads} "

@@ -40,7 +40,8 @@ def add_arguments(parser: argparse.ArgumentParser) -> None:
                         help="override CP_ASYNC (accepted; no effect on gfx950)")
     parser.add_argument("--cuda-graph", choices=("off", "auto", "always"), default=None,
                         help="override CUDA_GRAPH: capture the forward pass into a hipGraph")
-    parser.add_argument("--qkv-precision", choices=("fp16x2", "fp16x3", "fp16"), default=None,
+    parser.add_argument("--qkv-precision", choices=("auto", "fp16x2", "fp16x3", "fp16"),
+                        default=None,
                         help="override QKV_PRECISION: arithmetic of the QKV projection")
     parser.add_argument("--gelu-fp16", choices=("auto", "off"), default=None,
                         help="override GELU_FP16: store the GELU output in fp16 for ffn_out")

@@ -7,7 +7,7 @@ the value, not the setting. The thresholds below were re-derived for MI355X
 (256 CUs, 288 GB HBM3E) rather than carried over from the reference's card.
 
 Five knobs are new in this build:
-  QKV_PRECISION  arithmetic of the fused QKV projection (fp16x2, fp16x3, fp16)
+  QKV_PRECISION  arithmetic of the fused QKV projection (auto, fp16x2, fp16x3, fp16)
   GELU_FP16      whether linear_gelu stores its output as fp16 for ffn_out
   ROW_PACKING    whether a padded batch runs on its valid rows only
   RESIDUAL_EPILOGUE  whether out_proj and ffn_out add the residual stream
@@ -54,25 +54,27 @@ LINEAR_BIAS = "auto"
 _LINEAR_BIAS_MAX_ROWS = 1 << 31
 
 # Arithmetic of the fused QKV projection:
-#   "fp16x2" (default): the LayerNorm output as split fp16 hi+lo planes
-#            (~22 bits), the weight in fp16: two MFMA passes;
+#   "auto" (default): "fp16x2" when some query row attends to fewer than
+#          _QKV_SPLIT_MIN_KEYS keys (a causal mask, a short sequence, a short
+#          valid length), else "fp16";
+#   "fp16x2": the LayerNorm output as split fp16 hi+lo planes (~22 bits), the
+#          weight in fp16: two MFMA passes;
 #   "fp16x3": the weight split too: three passes, fp32-class products;
 #   "fp16":   one pass on fp16 operands.
 #
 # This is where the accuracy budget is spent. The layer's error is a sum of
-# fp16 operand roundings, and the tail of it (the elements that decide the
-# 2e-3 / 2% gate) is driven by the roundings that perturb the attention
-# SCORES: the LayerNorm output and the QKV weights, narrowed before the
-# projection. Emulated on the CPU against the fp32 reference (worst element
-# at the padded mass-batch config C5 / the wide config C4):
-#   one pass 2.02e-3 (one failing element in 41 M) / 1.69e-3;
-#   weight split only 1.98e-3 / 1.59e-3;
-#   LayerNorm output split only 1.65e-3 / 1.70e-3;
-#   both 1.62e-3 / 1.56e-3.
-# The LayerNorm rounding is the one that matters at C5, so "fp16x2" keeps
-# its split and drops the weight's: a third fewer MFMA passes and operand
-# bytes than "fp16x3" for a worst element within 10% of it.
-QKV_PRECISION = "fp16x2"
+# fp16 operand roundings, and the projection's roundings perturb the
+# attention SCORES; how much that moves the output depends on how many keys
+# a query row spreads its weight over. Measured on MI355X against the fp32
+# oracle, worst element with fp16x2 / fp16 QKV:
+#   C5 (1-16 keys a row): 1.90e-3 / 2.07e-3 with 2 failing elements;
+#   C3 (causal, row i sees i + 1 keys): 1.18e-3 / 1.67e-3;
+#   C2 (>= 256 keys a row): 0.98e-3 / 1.03e-3; C4 (2048 keys): 1.89e-3 / 1.77e-3
+#   (at C4 the worst element comes from ffn_in's fp16 operands, not QKV).
+# So the split planes are spent where rows see few keys and the one-pass
+# projection (half the MFMA work, the 256x256 tiles) runs elsewhere.
+QKV_PRECISION = "auto"
+_QKV_SPLIT_MIN_KEYS = 128
 # linear_bias `math` when the projection's input is not split planes (an
 # fp32 or fp16 x): the split arithmetic for either split setting.
 _QKV_MATH_CODE = {"fp16x3": 0, "fp16x2": 0, "fp16": -1}

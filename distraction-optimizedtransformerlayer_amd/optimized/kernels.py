@@ -45,6 +45,20 @@ _graph_io = None
 _stack_precision = False
 
 
+# Set by OptimizedTransformer.forward: whether some query row of this forward
+# attends to fewer than config._QKV_SPLIT_MIN_KEYS keys (what
+# QKV_PRECISION = "auto" resolves on).
+_qkv_few_keys = True
+
+
+def _qkv_precision() -> str:
+    """The QKV arithmetic this forward applies (config.QKV_PRECISION, "auto" resolved)."""
+    v = config.QKV_PRECISION
+    if v == "auto":
+        return "fp16x2" if _qkv_few_keys else "fp16"
+    return v
+
+
 def _lb() -> str:
     """config.LINEAR_BIAS as this forward applies it: "auto" becomes the split
     fp16x3 arithmetic ("tf32") inside a multi-block forward."""
@@ -187,7 +201,7 @@ def _normed_split_wanted() -> bool:
     output in the same bytes as fp32, already in the form the MFMA passes
     read.
     """
-    return (_lb() == "auto" and config.QKV_PRECISION in ("fp16x3", "fp16x2")
+    return (_lb() == "auto" and _qkv_precision() in ("fp16x3", "fp16x2")
             and config.NORMED_FP16 != "off")
 
 
@@ -219,11 +233,11 @@ def _add_layernorm_split(x: torch.Tensor, sub: torch.Tensor, norm):
 
 def _linear_bias_split(planes: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
                        out_half: bool = False) -> torch.Tensor:
-    """planes-as-x @ weight^T + bias in the split arithmetic config.QKV_PRECISION names."""
+    """planes-as-x @ weight^T + bias in the split arithmetic _qkv_precision() names."""
     kernels = _custom_kernels()
     if kernels is not None:
         out = kernels.linear_bias_split(planes, weight, bias, -1, out_half,
-                                        split_weight=config.QKV_PRECISION == "fp16x3")
+                                        split_weight=_qkv_precision() == "fp16x3")
         if out is not None:
             return out
     fallback_counts["linear_bias"] += 1
@@ -329,10 +343,10 @@ def _attention_wants_fp16() -> bool:
 
 
 def _qkv_math_code() -> int:
-    """linear_bias `math` for the QKV projection (config.QKV_PRECISION)."""
+    """linear_bias `math` for the QKV projection (_qkv_precision())."""
     if _lb() == "tf32":
         return config._GEMM_MATH_CODE["tf32"]
-    return config._QKV_MATH_CODE[config.QKV_PRECISION]
+    return config._QKV_MATH_CODE[_qkv_precision()]
 
 
 def _normed_wants_fp16(rows: int, width: int) -> bool:

@@ -139,12 +139,22 @@ class OptimizedTransformer(nn.Module):
     def forward(self, x: torch.Tensor,
                 valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         stacked = len(self.layers) > 1 and config.STACK_PRECISION == "auto"
-        saved = okernels._stack_precision
+        saved = (okernels._stack_precision, okernels._qkv_few_keys)
         okernels._stack_precision = stacked
+        okernels._qkv_few_keys = self._few_key_rows(x, self._mask_packing(valid_token_mask))
         try:
             return self._forward_dispatch(x, valid_token_mask)
         finally:
-            okernels._stack_precision = saved
+            okernels._stack_precision, okernels._qkv_few_keys = saved
+
+    def _few_key_rows(self, x: torch.Tensor, packing: Optional[RowPacking]) -> bool:
+        """Does some query row attend to fewer than config._QKV_SPLIT_MIN_KEYS
+        keys? Causal masking (row 0 sees one key), a short sequence, or a
+        padded batch's shortest valid length (from its packing, no extra sync)."""
+        limit = config._QKV_SPLIT_MIN_KEYS
+        if self.config.causal or x.shape[1] < limit:
+            return True
+        return packing is not None and not packing.trivial and packing.min_len < limit
 
     def _forward_dispatch(self, x: torch.Tensor,
                           valid_token_mask: Optional[torch.Tensor]) -> torch.Tensor:

@@ -41,6 +41,7 @@ class RowPacking:
     seq_len: int
     t_valid: int
     max_len: int
+    min_len: int
     idx: torch.Tensor   # int32 [t_valid]: packed row -> padded row b*S + s
     inv: torch.Tensor   # int32 [B*S]: padded row -> packed row, -1 for padding
     cu: torch.Tensor    # int32 [B+1]: sequence b is packed rows cu[b] .. cu[b+1]
@@ -56,7 +57,7 @@ class RowPacking:
 
     def empty_like(self) -> "RowPacking":
         """Uninitialised maps of the same sizes (a graph's static copy)."""
-        return RowPacking(self.batch, self.seq_len, self.t_valid, self.max_len,
+        return RowPacking(self.batch, self.seq_len, self.t_valid, self.max_len, self.min_len,
                           torch.empty_like(self.idx), torch.empty_like(self.inv),
                           torch.empty_like(self.cu))
 
@@ -79,13 +80,14 @@ def build_packing(mask: torch.Tensor) -> RowPacking:
     flat = mask.reshape(-1)
     if B * S == 0:
         z = torch.zeros(0, dtype=torch.int32, device=dev)
-        return RowPacking(B, S, 0, 0, z, z.clone(), torch.zeros(B + 1, dtype=torch.int32,
-                                                                 device=dev))
+        return RowPacking(B, S, 0, 0, 0, z, z.clone(), torch.zeros(B + 1, dtype=torch.int32,
+                                                                    device=dev))
     pos = torch.cumsum(flat.to(torch.int32), 0, dtype=torch.int32)  # inclusive
     counts = mask.sum(dim=1, dtype=torch.int32)
     cu = torch.zeros(B + 1, dtype=torch.int32, device=dev)
     cu[1:] = torch.cumsum(counts, 0, dtype=torch.int32)
-    t_valid, max_len = (int(v) for v in torch.stack([cu[-1], counts.max()]).tolist())
+    t_valid, max_len, min_len = (int(v) for v in
+                                 torch.stack([cu[-1], counts.max(), counts.min()]).tolist())
     minus_one = torch.full_like(pos, -1)
     inv = torch.where(flat, pos - 1, minus_one)
     # Scatter each valid row's padded index to its packed slot; padded rows
@@ -93,4 +95,4 @@ def build_packing(mask: torch.Tensor) -> RowPacking:
     target = torch.where(flat, pos - 1, torch.full_like(pos, t_valid)).long()
     idx = torch.empty(t_valid + 1, dtype=torch.int32, device=dev)
     idx.scatter_(0, target, torch.arange(B * S, dtype=torch.int32, device=dev))
-    return RowPacking(B, S, t_valid, max_len, idx[:t_valid], inv, cu)
+    return RowPacking(B, S, t_valid, max_len, min_len, idx[:t_valid], inv, cu)
