@@ -9,7 +9,8 @@ using gemm_dma::dispatch_tile;
 
 // Tile choice, from sweeps of every GEMM of the five layer configs on MI355X
 // (passes = planes multiplied: 1 + split x + split W):
-//   * one pass: 256x256 with 128-byte K rows for K >= 2048 once that gives a
+//   * one pass: 256x256 with 8 waves for wide products (N >= 4096, K >= 1024);
+//     256x256 with 128-byte K rows for K >= 2048 once that gives a
 //     workgroup per CU; else the 128x128 two-stage tile (two workgroups a
 //     CU) when it fills the CUs four times over, or at short K; else
 //     128x64, then 64x64;
@@ -21,6 +22,10 @@ using gemm_dma::dispatch_tile;
 int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     if (passes == 1) {
+        // wide products: the 8-wave 256x256 tile (two waves a SIMD hide each
+        // other's DMA issue stalls): C4 QKV 225 -> 218 us, C4 ffn_in 312 ->
+        // 295, C3 ffn_in 51 -> 47; at N = 2048 it loses (out_proj 74 -> 79)
+        if (K >= 1024 && N >= 4096 && tiles(256, 256) >= 240) return 15;
         if (K >= 2048 && tiles(256, 256) >= 240) return 9;
         if (tiles(128, 128) >= 960) return 12;
         if (tiles(128, 128) >= 240 && K <= 1024) return 12;

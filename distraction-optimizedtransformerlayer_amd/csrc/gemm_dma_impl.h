@@ -73,14 +73,16 @@ __device__ __forceinline__ void tile_of(int64_t id, int64_t nm, int64_t nn, int6
     nt = r / gsize;
 }
 
-template <int BM, int BN, int BK, int MODE>
+// NWV wavefronts a workgroup: 4 (2 x 2, one per SIMD) or 8 (2 x 4, two per
+// SIMD, so one wave's MFMAs run while its partner waits on LDS or the DMA).
+template <int BM, int BN, int BK, int MODE, int NWV = 4>
 struct DmaLayout {
     // rows of BK halves in one stage: A, W, then lo(W) (MODE & 1), lo(A) (MODE & 2)
     static constexpr bool SW = (MODE & 1) != 0;
     static constexpr bool SA = (MODE & 2) != 0;
     static constexpr int CPR = BK / 8;               // 16-byte chunks per row
     static constexpr int ROWS_PER_DMA = 64 / CPR;    // rows one wave instruction fills
-    static constexpr int ROWS_PER_ROUND = 4 * ROWS_PER_DMA;
+    static constexpr int ROWS_PER_ROUND = NWV * ROWS_PER_DMA;
     static constexpr int SWZ_DIV = 256 / (BK * 2);   // rows per 256-byte bank sweep
     static constexpr int A_ROW = 0;
     static constexpr int W_ROW = BM;
@@ -93,13 +95,14 @@ struct DmaLayout {
     __device__ __forceinline__ static int swz(int row) { return (row / SWZ_DIV) % CPR; }
 };
 
-template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT>
+template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT, int NWV = 4>
 struct DmaGemm {
-    using L = DmaLayout<BM, BN, BK, MODE>;
+    using L = DmaLayout<BM, BN, BK, MODE, NWV>;
+    static constexpr int WGN = NWV / 2;          // waves across N (2 or 4); 2 across M
     static constexpr bool SPLIT = (MODE & 3) != 0;
     // MODE 4: bf16 operands (the LDS stages hold 16-bit values either way), one pass
     static constexpr bool BF16 = MODE == 4;
-    static constexpr int WM = BM / 2, WN = BN / 2;
+    static constexpr int WM = BM / 2, WN = BN / WGN;
     static constexpr int TM = WM / 32, TN = WN / 32;
 
     const _Float16* __restrict__ A;
@@ -180,26 +183,68 @@ struct DmaGemm {
     }
 
     // Multiply the tile in `stage`; if `more`, issue tile kt_next into
-    // `next` meanwhile, one slice of its DMAs after each row of MFMAs, so the
-    // vector-memory issue (which stalls while the CU's load queue is full)
-    // runs under the matrix cores instead of ahead of them.
+    // `next` meanwhile. Two schedules, both measured on MI355X:
+    //   * the next tile's DMAs all go out during the first 16-deep k step,
+    //     one after each MFMA (the vector-memory issue stalls while the CU's
+    //     load queue is full; behind an MFMA the stall is hidden), so the
+    //     stage's whole round trip (~0.8 us for 64 KiB) runs under the
+    //     remaining three quarters of the tile's MFMAs. Spread evenly over
+    //     the tile instead, the last slice was issued at its end and the
+    //     barrier then waited out its full latency: the kernel took the DMA
+    //     time plus the MFMA time (C4 QKV 207 us against 125 + 83);
+    //   * the fragments of k step ks + 1 are read from LDS before the MFMAs
+    //     of step ks are issued, so their latency too runs under MFMAs.
+    __device__ __forceinline__ void load_frags(const _Float16* stage, int ks, half8 (&a)[TM],
+                                               half8 (&b)[TN]) const {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[i] = frag(stage + L::A_ROW * BK, wm * WM + i * 32 + lr, ks);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) b[j] = frag(stage + L::W_ROW * BK, wn * WN + j * 32 + lr, ks);
+    }
+
     __device__ __forceinline__ void compute(const _Float16* stage, _Float16* next, int64_t kt_next,
                                             bool more) {
-        constexpr int SLOTS = KS * TM;
+        // k steps the DMAs are spread over: the first only with two stages
+        // (the next barrier waits for them); with more stages each tile has
+        // NS - 2 further tiles' MFMAs to land, and an even spread issues more
+        // gently.
+        constexpr int ISSUE_KS = NS == 2 ? 1 : KS;
+        constexpr int PER = TM * TN;                    // MFMAs a k step
+        constexpr int SLOTS = ISSUE_KS * PER;
+        constexpr int NF = TM + TN;                     // fragment reads a k step
+        constexpr int ROUNDS = PER > NF ? PER : NF;
+        half8 fa[2][TM], fb[2][TN];
+        load_frags(stage, 0, fa[0], fb[0]);
         static_for<0, KS>([&](auto kk) {
             constexpr int ks = decltype(kk)::value;
-            half8 a[TM], b[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) a[i] = frag(stage + L::A_ROW * BK, wm * WM + i * 32 + lr, ks);
-#pragma unroll
-            for (int j = 0; j < TN; ++j) b[j] = frag(stage + L::W_ROW * BK, wn * WN + j * 32 + lr, ks);
-            static_for<0, TM>([&](auto ii) {
-                constexpr int i = decltype(ii)::value;
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
+            constexpr int cur = ks & 1;
+            half8 (&a)[TM] = fa[cur];
+            half8 (&b)[TN] = fb[cur];
+            // Round m: MFMA m of this step, fragment read m of the next step,
+            // DMA slice m. The scheduling barrier after each round keeps the
+            // compiler from regrouping them: left free it sank the reads of
+            // step ks + 1 below the MFMAs of step ks (less register pressure),
+            // and every step then began by waiting out a full LDS read
+            // latency with the matrix core idle -- the loop ran at ~55% of
+            // the MFMA rate with no global traffic at all.
+            static_for<0, ROUNDS>([&](auto mm) {
+                constexpr int m = decltype(mm)::value;
+                if constexpr (m < PER) {
+                    constexpr int i = m / TN, j = m % TN;
                     acc[i][j] = mma(b[j], a[i], acc[i][j]);
-                constexpr int slot = ks * TM + i;
-                if (more) issue_range<slot * NDMA / SLOTS, (slot + 1) * NDMA / SLOTS>(next, kt_next);
+                }
+                if constexpr (ks + 1 < KS && m < NF) {
+                    if constexpr (m < TM)
+                        fa[cur ^ 1][m] = frag(stage + L::A_ROW * BK, wm * WM + m * 32 + lr, ks + 1);
+                    else
+                        fb[cur ^ 1][m - TM] =
+                            frag(stage + L::W_ROW * BK, wn * WN + (m - TM) * 32 + lr, ks + 1);
+                }
+                if constexpr (ks < ISSUE_KS && m < PER) {
+                    constexpr int slot = ks * PER + m;
+                    if (more) issue_range<slot * NDMA / SLOTS, (slot + 1) * NDMA / SLOTS>(next, kt_next);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             });
             if constexpr (L::SW) {
                 half8 bl[TN];
@@ -240,13 +285,13 @@ struct DmaGemm {
     }
 };
 
-template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT>
-__global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
+template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT, int NWV = 4>
+__global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
     const _Float16* __restrict__ A, const _Float16* __restrict__ Alo,
     const _Float16* __restrict__ W, const _Float16* __restrict__ Wlo,
     const float* __restrict__ bias, const float* __restrict__ R, void* __restrict__ C, int64_t M,
     int64_t N, int64_t K) {
-    using G = DmaGemm<BM, BN, BK, NS, MODE, ACT, OUTT>;
+    using G = DmaGemm<BM, BN, BK, NS, MODE, ACT, OUTT, NWV>;
     using L = typename G::L;
     static_assert(NS >= 2 && NS <= 8, "2 to 8 stages");
     static_assert((NS - 2) * L::LOADS < 64, "vmcnt is 6 bits");
@@ -267,8 +312,8 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     g.M = M; g.N = N; g.K = K;
     g.lane = threadIdx.x & 63;
     g.wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    g.wm = g.wave >> 1;
-    g.wn = g.wave & 1;
+    g.wm = g.wave / G::WGN;
+    g.wn = g.wave % G::WGN;
     g.lr = g.lane & 31;
     g.lg = g.lane >> 5;
     int64_t mt, nt;
@@ -301,7 +346,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     // barriers publish them): read in the epilogue from LDS, they do not wait
     // behind the epilogue's own global stores the way a global load would.
     __shared__ __attribute__((aligned(16))) float sbias[BN];
-    for (int c = threadIdx.x; c < BN; c += kThreads) {
+    for (int c = threadIdx.x; c < BN; c += NWV * 64) {
         const int64_t col = g.n0 + c;
         sbias[c] = col < N ? bias[col] : 0.f;
     }
@@ -412,11 +457,11 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
     }
 }
 
-template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT>
+template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT, int NWV = 4>
 void launch_dma(const DmaArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, MODE, ACT, OUTT>),
-                       dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, a.stream, a.A,
+    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, MODE, ACT, OUTT, NWV>),
+                       dim3(static_cast<unsigned>(tiles)), dim3(NWV * 64), 0, a.stream, a.A,
                        a.Alo, a.W, a.Wlo, a.bias, a.R, a.C, a.M, a.N, a.K);
 }
 
@@ -490,6 +535,16 @@ bool dispatch_tile(const DmaArgs& a, int tile) {
         case 14:
             if constexpr (PASSES == 1) { launch_dma<192, 128, 64, 3, MODE, ACT, OUTT>(a); return true; }
             else if constexpr (PASSES == 2) { launch_dma<192, 128, 64, 2, MODE, ACT, OUTT>(a); return true; }
+            return false;
+        // 8 waves (two per SIMD), each a 128x64 block of the tile.
+        case 15:  // 256x256, 128-byte K rows, 2 stages of 64 KiB
+            if constexpr (PASSES == 1) { launch_dma<256, 256, 64, 2, MODE, ACT, OUTT, 8>(a); return true; }
+            return false;
+        case 16:  // 256x256, 64-byte K rows, 4 stages of 32 KiB
+            if constexpr (PASSES == 1) { launch_dma<256, 256, 32, 4, MODE, ACT, OUTT, 8>(a); return true; }
+            return false;
+        case 17:  // 256x128, 128-byte K rows, 3 stages of 48 KiB
+            if constexpr (PASSES == 1) { launch_dma<256, 128, 64, 3, MODE, ACT, OUTT, 8>(a); return true; }
             return false;
     }
     return false;

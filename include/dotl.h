@@ -169,8 +169,10 @@ int dotl_weight_split(const float* w, void* w_hi, void* w_lo, int64_t n, void* s
  *             fit two workgroups per CU; 9-13: 256x256 [one pass], 128x128,
  *             256x128 [one pass], 128x128 [one pass, two stages], 128x64 with
  *             128-byte K rows; 14: 192x128 with 128-byte K rows [one or two
- *             passes]); 100 + id (id <= 4) forces the register-staged kernel
- *             (for measurement)
+ *             passes]; 15-17: 8 waves a workgroup, two per SIMD, [one pass]:
+ *             256x256 with 128-byte K rows, 256x256 with 64-byte K rows,
+ *             256x128 with 128-byte K rows); 100 + id (id <= 4) forces the
+ *             register-staged kernel (for measurement)
  *   fp16 / split-fp16 x with K % 64 == 0 runs the LDS-DMA pipelined kernel;
  *   anything else the register-staged one. Declines when K % 8 != 0, or a
  *   DOTL_F16X2 x with K % 64 != 0.

@@ -390,7 +390,7 @@ def test_layernorm_split_planes(kernels, rows, D):
 DMA_SHAPES = [(300, 200, 128), (1000, 1024, 256), (64, 2048, 512), (513, 384, 64)]
 
 
-ALL_TILES = [-1] + list(range(15))
+ALL_TILES = [-1] + list(range(18))
 SPLIT_TILES = [-1, 0, 2, 4, 5, 7, 8, 10, 13]   # the tiles built for split passes
 TWO_PASS_TILES = SPLIT_TILES + [14]            # 192x128: one or two passes, not three
 
