@@ -108,6 +108,41 @@ __global__ void lds_dma_probe_kernel(const int32_t* __restrict__ src, int32_t* _
     for (int i = lane; i < 512; i += 64) out[i] = region[i];
 }
 
+// Sustained MFMA rate: each wave chains `iters` rounds of 16 independent
+// v_mfma_f32_32x32x16_f16 on register operands (4 A x 4 B fragments, no
+// memory traffic). random != 0 fills the fragments with random values, as a
+// GEMM's are; on MI355X the matrix cores then draw enough power to pull the
+// clock from ~2.2 to ~1.7 GHz, and that -- not the datasheet rate -- is the
+// roof every MFMA kernel here runs against.
+__global__ __launch_bounds__(256) void mfma_ceiling_kernel(int iters, int random, float* sink) {
+    floatx16 acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = floatx16{};
+    half8 a[4], b[4];
+    uint32_t st = threadIdx.x * 7919u + blockIdx.x * 104729u + 1u;
+    for (int r = 0; r < 4; ++r)
+        for (int e = 0; e < 8; ++e) {
+            float x = e * 0.25f, y = e * 0.5f;
+            if (random) {
+                st = st * 1664525u + 1013904223u;
+                x = (((st >> 9) & 0x3fff) / 16384.0f - 0.5f) * 4.f;
+                st = st * 1664525u + 1013904223u;
+                y = (((st >> 9) & 0x3fff) / 16384.0f - 0.5f) * 4.f;
+            }
+            a[r][e] = static_cast<_Float16>(x);
+            b[r][e] = static_cast<_Float16>(y);
+        }
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[i % 4], a[i / 4], acc[i], 0, 0, 0);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s += acc[i][threadIdx.x & 15];
+    if (s == 1234.5f) sink[0] = s;   // keeps the products live; never true in practice
+}
+
 }  // namespace
 }  // namespace dotl
 
@@ -138,6 +173,18 @@ int dotl_mfma_layout_probe(int32_t* out, void* stream) {
     DOTL_REQUIRE(out != nullptr, "mfma_layout_probe: null output");
     hipLaunchKernelGGL(dotl::mfma_probe_kernel, dim3(1), dim3(64), 0, dotl::as_stream(stream), out);
     return dotl::check_launch("mfma_layout_probe");
+}
+
+int dotl_mfma_ceiling_probe(int64_t workgroups, int32_t iters, int32_t random_operands, float* sink,
+                            void* stream) {
+    dotl::clear_error();
+    DOTL_REQUIRE(sink != nullptr, "mfma_ceiling_probe: null sink");
+    DOTL_REQUIRE(workgroups >= 1 && workgroups <= 0x7fffffff && iters >= 0 && iters <= (1 << 20),
+                 "mfma_ceiling_probe: workgroups must be in [1, 2^31) and iters in [0, 2^20]");
+    hipLaunchKernelGGL(dotl::mfma_ceiling_kernel, dim3(static_cast<unsigned>(workgroups)), dim3(256),
+                       0, dotl::as_stream(stream), static_cast<int>(iters),
+                       random_operands ? 1 : 0, sink);
+    return dotl::check_launch("mfma_ceiling_probe");
 }
 
 int dotl_lds_dma_probe(const int32_t* src, int32_t* out, void* stream) {

@@ -22,11 +22,11 @@ using gemm_dma::dispatch_tile;
 int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     if (passes == 1) {
-        // wide products: the 8-wave 256x256 tile (two waves a SIMD hide each
-        // other's DMA issue stalls): C4 QKV 225 -> 218 us, C4 ffn_in 312 ->
-        // 295, C3 ffn_in 51 -> 47; at N = 2048 it loses (out_proj 74 -> 79)
-        if (K >= 1024 && N >= 4096 && tiles(256, 256) >= 240) return 15;
-        if (K >= 2048 && tiles(256, 256) >= 240) return 9;
+        // large products: the 8-wave 256x256 tile (two waves a SIMD hide
+        // each other's waits) with the LDS-staged epilogue, measured on
+        // MI355X against the 4-wave one: C4 QKV 181 vs 202 us, ffn_in 275 vs
+        // 292, ffn_out (+ residual) 241 vs 242, out_proj 78 vs 80
+        if (K >= 1024 && tiles(256, 256) >= 240) return 15;
         if (tiles(128, 128) >= 960) return 12;
         if (tiles(128, 128) >= 240 && K <= 1024) return 12;
         if (tiles(128, 64) >= 200) return 13;

@@ -9,12 +9,19 @@
 // MI355X design:
 //   * no staging registers: each lane's 16-byte load lands directly in LDS
 //     (the wave's 64 lanes fill one contiguous 1 KiB run, lane l at +16 l),
-//     so the pipeline can be 4-8 stages deep (up to 144 KiB of the CU's
-//     160 KiB LDS) without spending VGPRs. Measured on MI355X, a CU's
-//     operand stream is latency-bound: ~1.6 us per 64 KiB batch in flight,
-//     so feeding a 256x256 tile at the MFMA rate takes ~100 KiB in flight.
-//     K tiles are therefore 32 deep (BK = 32: 32 KiB per 256x256 stage) and
-//     the stages many, NS - 1 of them in flight while one is multiplied;
+//     so the pipeline can be 2-8 stages deep (up to 144 KiB of the CU's
+//     160 KiB LDS) without spending VGPRs. Measured on MI355X with the C4
+//     QKV product's address stream alone (1.5 GB of L2 -> LDS): 128-byte K
+//     rows (BK = 64, each 8 lanes one whole cache line) stream it in 74 us
+//     with one 64 KiB stage in flight a workgroup and two workgroups a CU,
+//     70 us with two stages in flight; 64-byte rows (BK = 32) take 114 us,
+//     each line being fetched twice. One workgroup a CU with one stage in
+//     flight (the 256x256 tile's 2 x 64 KiB) takes 125 us: the stage's
+//     round trip, ~1.3 us, is what the tile's MFMAs must cover;
+//   * the MFMA ceiling with data: 32x32x16 f16 products on random operands
+//     pull the clock down to ~1.7 GHz (2.2 GHz on constant ones), ~1.5
+//     PFLOP/s sustained, so ~60% of the 2.5 PFLOP/s datasheet figure is the
+//     practical roof of every kernel here;
 //   * each stage is its own __shared__ array and the K loop is unrolled by
 //     NS, so every LDS read names a stage the in-flight DMA provably does not
 //     write: the compiler then adds no conservative vmcnt(0) before the reads;
@@ -37,13 +44,14 @@
 //     x*W + 2^-12 x*lo(W) (x exact in fp16); 2 hi(x)*W + 2^-12 lo(x)*W (x
 //     given as fp16 hi/lo planes, W in fp16); 3 all three products: the
 //     lo terms in a second fp32 accumulator;
-//   * 2 x 2 wavefronts, each a (BM/2) x (BN/2) block of 32x32 accumulators,
-//     issued as W x A^T so every accumulator holds a C^T tile: each lane then
-//     owns runs of 4 consecutive output columns of one row, and the epilogue
-//     (bias from LDS, GELU, narrowing) stores them 16 or 8 bytes at a time
-//     from one row address per tile. The epilogue's cost matters here: with
-//     one workgroup per CU nothing overlaps it, and at the configs' short K
-//     (256-512) it was costing more than the MFMAs.
+//   * 2 x 2 (or 2 x 4) wavefronts, each a (BM/2) x (BN/WGN) block of 32x32
+//     accumulators, issued as W x A^T so every accumulator holds a C^T
+//     tile: each lane owns runs of 4 consecutive output columns of one row.
+//     The epilogue transposes the tile through the (then free) stage
+//     buffers so that bias, GELU, residual loads and output stores run on
+//     row-contiguous 16-byte chunks. Its cost matters: with one workgroup
+//     per CU nothing overlaps it, and at the configs' short K (256-512) it
+//     was costing more than the MFMAs.
 #include <type_traits>
 
 #include "dotl_dma.h"
@@ -184,14 +192,13 @@ struct DmaGemm {
 
     // Multiply the tile in `stage`; if `more`, issue tile kt_next into
     // `next` meanwhile. Two schedules, both measured on MI355X:
-    //   * the next tile's DMAs all go out during the first 16-deep k step,
-    //     one after each MFMA (the vector-memory issue stalls while the CU's
-    //     load queue is full; behind an MFMA the stall is hidden), so the
-    //     stage's whole round trip (~0.8 us for 64 KiB) runs under the
-    //     remaining three quarters of the tile's MFMAs. Spread evenly over
-    //     the tile instead, the last slice was issued at its end and the
-    //     barrier then waited out its full latency: the kernel took the DMA
-    //     time plus the MFMA time (C4 QKV 207 us against 125 + 83);
+    //   * with two stages the next tile's DMAs all go out during the first
+    //     two 16-deep k steps, one after an MFMA (the vector-memory issue
+    //     stalls while the CU's load queue is full; behind an MFMA the stall
+    //     is hidden), so the stage's round trip (~1.3 us for 64 KiB, one
+    //     stage in flight a CU) runs under the tile's remaining MFMAs.
+    //     Spread evenly over the tile, the last slice was issued at its end
+    //     and the barrier waited out its full latency;
     //   * the fragments of k step ks + 1 are read from LDS before the MFMAs
     //     of step ks are issued, so their latency too runs under MFMAs.
     __device__ __forceinline__ void load_frags(const _Float16* stage, int ks, half8 (&a)[TM],
@@ -204,11 +211,11 @@ struct DmaGemm {
 
     __device__ __forceinline__ void compute(const _Float16* stage, _Float16* next, int64_t kt_next,
                                             bool more) {
-        // k steps the DMAs are spread over: the first only with two stages
-        // (the next barrier waits for them); with more stages each tile has
-        // NS - 2 further tiles' MFMAs to land, and an even spread issues more
-        // gently.
-        constexpr int ISSUE_KS = NS == 2 ? 1 : KS;
+        // k steps the DMAs are spread over: the first two with two stages
+        // (the next barrier waits for them; on MI355X two beat one by 1-4%
+        // and all four lose 3-5%); with more stages each tile has NS - 2
+        // further tiles' MFMAs to land, and an even spread issues more gently.
+        constexpr int ISSUE_KS = NS == 2 ? (KS < 2 ? KS : 2) : KS;
         constexpr int PER = TM * TN;                    // MFMAs a k step
         constexpr int SLOTS = ISSUE_KS * PER;
         constexpr int NF = TM + TN;                     // fragment reads a k step
@@ -404,56 +411,184 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
     // Epilogue. The MFMAs were issued as W x A^T, so each 32x32 accumulator
     // holds a tile of C^T: lane l owns C row (l % 32) of the tile, and
     // registers 4g .. 4g+3 hold the four consecutive C columns
-    // 8g + 4 (l / 32) + 0..3 -- one 16-byte (fp32) or 8-byte (fp16) store.
+    // 8g + 4 (l / 32) + 0..3. Stored from there, one wave instruction would
+    // touch 32 rows in 16- or 32-byte pieces (and so would the residual's
+    // loads): on MI355X an fp32 output then cost more than the MFMAs of a
+    // short-K tile (C4 ffn_in shape: 345 us fp32 out, 272 fp16). So the
+    // tile goes through LDS, which the finished K loop leaves free: each
+    // wave writes its raw accumulators into the stage buffers, then every
+    // thread takes row-contiguous 16-byte chunks -- a wave instruction
+    // covers 1 KiB of one row -- adds bias, activation and residual in fp32
+    // (the same operations in the same order as per element before), and
+    // stores. A 256 x 256 fp32 tile takes two rounds of the 2 x 64 KiB
+    // stages. The 16-byte chunks are XOR-swizzled by row (chunk ^ row % 16)
+    // so that both the column writes (16 rows a pass) and the row reads are
+    // free of bank conflicts.
+    using TO = typename std::conditional<
+        OUTT == DOTL_F32, float,
+        typename std::conditional<OUTT == DOTL_BF16, __bf16, _Float16>::type>::type;
     const bool vec_ok = (N & 3) == 0;
+    // The direct epilogue (each lane stores its own runs of 4 columns) for a
+    // GELU with a 16-bit output: there the staged one measured no better
+    // (C4 ffn_in shape 288 us either way on the 8-wave tile) and worse on
+    // the 4-wave ones, whose waves have no partner to overlap the transpose.
+    constexpr bool STAGED = !(ACT == DOTL_ACT_GELU && OUTT != DOTL_F32);
+    if constexpr (!STAGED) {
 #pragma unroll
-    for (int i = 0; i < G::TM; ++i) {
-        const int64_t row = g.m0 + g.wm * G::WM + i * 32 + g.lr;
-        if (row >= M) continue;
+        for (int i = 0; i < G::TM; ++i) {
+            const int64_t row = g.m0 + g.wm * G::WM + i * 32 + g.lr;
+            if (row >= M) continue;
 #pragma unroll
-        for (int j = 0; j < G::TN; ++j) {
+            for (int j = 0; j < G::TN; ++j) {
 #pragma unroll
-            for (int grp = 0; grp < 4; ++grp) {
-                const int cl = g.wn * G::WN + j * 32 + 8 * grp + 4 * g.lg;  // tile-local column
-                const int64_t col = g.n0 + cl;
-                float v[4];
+                for (int grp = 0; grp < 4; ++grp) {
+                    const int cl = g.wn * G::WN + j * 32 + 8 * grp + 4 * g.lg;  // tile-local column
+                    const int64_t col = g.n0 + cl;
+                    float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float a = g.acc[i][j][4 * grp + e];
-                    if constexpr (G::SPLIT) a += g.acc2[i][j][4 * grp + e] * kLoUnscale;
-                    a += sbias[cl + e];
-                    if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
-                    v[e] = a;
-                }
-                if constexpr (OUTT == DOTL_F32) {
-                    // residual stream: out = R + act(x W^T + b), the add the
-                    // following LayerNorm would otherwise do (same fp32 sum)
-                    if (R != nullptr) {
-                        const float* rrow = R + row * N + col;
-                        if (vec_ok && col + 4 <= N) {
-                            const float4 r4 = *reinterpret_cast<const float4*>(rrow);
-                            v[0] = r4.x + v[0]; v[1] = r4.y + v[1];
-                            v[2] = r4.z + v[2]; v[3] = r4.w + v[3];
-                        } else {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                if (col + e < N) v[e] = rrow[e] + v[e];
-                        }
+                    for (int e = 0; e < 4; ++e) {
+                        float a = g.acc[i][j][4 * grp + e];
+                        if constexpr (G::SPLIT) a += g.acc2[i][j][4 * grp + e] * kLoUnscale;
+                        a += sbias[cl + e];
+                        if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
+                        v[e] = a;
                     }
-                }
-                using TO = typename std::conditional<
-                    OUTT == DOTL_F32, float,
-                    typename std::conditional<OUTT == DOTL_BF16, __bf16, _Float16>::type>::type;
-                TO* crow = static_cast<TO*>(C) + row * N;
-                if (vec_ok && col + 4 <= N) {
-                    store4f(crow + col, make_float4(v[0], v[1], v[2], v[3]));
-                } else {
+                    TO* crow = static_cast<TO*>(C) + row * N;
+                    if (vec_ok && col + 4 <= N) {
+                        store4f(crow + col, make_float4(v[0], v[1], v[2], v[3]));
+                    } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (col + e < N) crow[col + e] = from_f32<TO>(v[e]);
+                        for (int e = 0; e < 4; ++e)
+                            if (col + e < N) crow[col + e] = from_f32<TO>(v[e]);
+                    }
                 }
             }
         }
+        return;
+    } else {
+    constexpr int BUF_BYTES = SZ * 2;
+    constexpr int ROW_BYTES = BN * 4;
+    constexpr int RPB = (BUF_BYTES / ROW_BYTES) / 32 * 32;   // tile rows a stage buffer holds
+    constexpr int CPR = BN / 4;                              // 16-byte chunks a row
+    static_assert(RPB >= 32, "a stage buffer must hold 32 fp32 tile rows");
+    static_assert(CPR >= 16 && (64 % CPR == 0 || CPR % 64 == 0), "row chunks");
+    constexpr int RR = RPB * NS;                            // tile rows a round holds
+    constexpr int ROUNDS = (BM + RR - 1) / RR;
+    constexpr int THREADS = NWV * 64;
+    auto buf = [&](int b) -> float* {
+        _Float16* p = st0;
+        if (b == 1) p = st1;
+        if constexpr (NS > 2) if (b == 2) p = st2;
+        if constexpr (NS > 3) if (b == 3) p = st3;
+        if constexpr (NS > 4) if (b == 4) p = st4;
+        if constexpr (NS > 5) if (b == 5) p = st5;
+        if constexpr (NS > 6) if (b == 6) p = st6;
+        if constexpr (NS > 7) if (b == 7) p = st7;
+        return reinterpret_cast<float*>(p);
+    };
+    stage_barrier();   // every wave is done reading the stages
+    static_for<0, ROUNDS>([&](auto qq) {
+        constexpr int q = decltype(qq)::value;
+        constexpr int r_lo = q * RR;
+        constexpr int r_hi = (q + 1) * RR < BM ? (q + 1) * RR : BM;
+        constexpr int CHUNKS = (r_hi - r_lo) * CPR;
+        static_assert(CHUNKS % THREADS == 0, "round chunks");
+        constexpr int PER_T = CHUNKS / THREADS;
+        // The round's residual, loaded first: its HBM latency then runs
+        // under the LDS writes and the barrier instead of stalling the
+        // store loop once per batch.
+        float4 res[OUTT == DOTL_F32 ? PER_T : 1];
+        if constexpr (OUTT == DOTL_F32) {
+            if (R != nullptr) {
+#pragma unroll
+                for (int u = 0; u < PER_T; ++u) {
+                    const int c = threadIdx.x + u * THREADS;
+                    const int64_t row = g.m0 + r_lo + c / CPR;
+                    const int64_t col = g.n0 + (c % CPR) * 4;
+                    res[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (row < M) {
+                        const float* rrow = R + row * N + col;
+                        if (vec_ok && col + 4 <= N) {
+                            res[u] = *reinterpret_cast<const float4*>(rrow);
+                        } else {
+                            if (col + 0 < N) res[u].x = rrow[0];
+                            if (col + 1 < N) res[u].y = rrow[1];
+                            if (col + 2 < N) res[u].z = rrow[2];
+                            if (col + 3 < N) res[u].w = rrow[3];
+                        }
+                    }
+                }
+            }
+        }
+        if constexpr (q > 0) stage_barrier();   // the previous round's reads are done
+        // write: this wave's 32-row groups that fall in the round
+#pragma unroll
+        for (int i = 0; i < G::TM; ++i) {
+            const int gb = g.wm * G::WM + i * 32;   // wave-uniform
+            if (gb < r_lo || gb >= r_hi) continue;
+            const int b = (gb - r_lo) / RPB;
+            const int rb = (gb - r_lo) % RPB + g.lr;
+            float* base = buf(b) + rb * BN;
+#pragma unroll
+            for (int j = 0; j < G::TN; ++j) {
+#pragma unroll
+                for (int grp = 0; grp < 4; ++grp) {
+                    const int chunk = (g.wn * G::WN + j * 32 + 8 * grp) / 4 + g.lg;
+                    float4 v;
+                    v.x = g.acc[i][j][4 * grp + 0];
+                    v.y = g.acc[i][j][4 * grp + 1];
+                    v.z = g.acc[i][j][4 * grp + 2];
+                    v.w = g.acc[i][j][4 * grp + 3];
+                    if constexpr (G::SPLIT) {
+                        v.x += g.acc2[i][j][4 * grp + 0] * kLoUnscale;
+                        v.y += g.acc2[i][j][4 * grp + 1] * kLoUnscale;
+                        v.z += g.acc2[i][j][4 * grp + 2] * kLoUnscale;
+                        v.w += g.acc2[i][j][4 * grp + 3] * kLoUnscale;
+                    }
+                    *reinterpret_cast<float4*>(base + ((chunk ^ (rb & 15)) * 4)) = v;
+                }
+            }
+        }
+        stage_barrier();
+        // read + store: row-contiguous chunks of rows [r_lo, r_hi)
+#pragma unroll
+        for (int u = 0; u < PER_T; ++u) {
+            const int c = threadIdx.x + u * THREADS;
+            const int rl = c / CPR;                 // row within the round
+            const int cc = c % CPR;                 // logical chunk
+            const int b = rl / RPB;
+            const int rb = rl % RPB;
+            const int64_t row = g.m0 + r_lo + rl;
+            const int cl = cc * 4;                  // tile-local column
+            const int64_t col = g.n0 + cl;
+            if (row >= M) continue;
+            const float4 a4 =
+                *reinterpret_cast<const float4*>(buf(b) + rb * BN + ((cc ^ (rb & 15)) * 4));
+            float v[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float a = v[e] + sbias[cl + e];
+                if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
+                v[e] = a;
+            }
+            if constexpr (OUTT == DOTL_F32) {
+                // residual stream: out = R + act(x W^T + b), the add the
+                // following LayerNorm would otherwise do (same fp32 sum)
+                if (R != nullptr) {
+                    v[0] = res[u].x + v[0]; v[1] = res[u].y + v[1];
+                    v[2] = res[u].z + v[2]; v[3] = res[u].w + v[3];
+                }
+            }
+            TO* crow = static_cast<TO*>(C) + row * N;
+            if (vec_ok && col + 4 <= N) {
+                store4f(crow + col, make_float4(v[0], v[1], v[2], v[3]));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < N) crow[col + e] = from_f32<TO>(v[e]);
+            }
+        }
+    });
     }
 }
 

@@ -54,7 +54,7 @@ DOTL_MATH_FP16X2 = 2
 # Every symbol include/dotl.h declares.
 EXPORTED_SYMBOLS = (
     "dotl_last_error", "dotl_abi_version", "dotl_target", "dotl_smoke_test_identity",
-    "dotl_mfma_layout_probe", "dotl_layernorm", "dotl_weight_split", "dotl_linear",
+    "dotl_mfma_layout_probe", "dotl_mfma_ceiling_probe", "dotl_layernorm", "dotl_weight_split", "dotl_linear",
     "dotl_attention_forward", "dotl_ffn_block", "dotl_wmma_set_fp16", "dotl_wmma_fp16",
     "dotl_wmma_set_cp_async", "dotl_wmma_cp_async_mode", "dotl_lds_dma_probe",
     "dotl_attention_set_pipeline", "dotl_linear_residual", "dotl_bind_io",
@@ -102,6 +102,8 @@ def _declare(lib) -> None:
     lib.dotl_smoke_test_identity.argtypes = [vp, vp, i64, vp]
     lib.dotl_mfma_layout_probe.restype = i32
     lib.dotl_mfma_layout_probe.argtypes = [vp, vp]
+    lib.dotl_mfma_ceiling_probe.restype = i32
+    lib.dotl_mfma_ceiling_probe.argtypes = [i64, i32, i32, vp, vp]
     lib.dotl_lds_dma_probe.restype = i32
     lib.dotl_lds_dma_probe.argtypes = [vp, vp, vp]
     lib.dotl_layernorm.restype = i32
@@ -238,6 +240,32 @@ class Kernels:
         out = torch.empty(1280, dtype=torch.int32, device=device or "cuda")
         self._check(self._lib.dotl_mfma_layout_probe(out.data_ptr(), self._stream(out.device)))
         return out
+
+    def mfma_ceiling_us(self, workgroups, iters, random_operands=True, reps=20, warmup=10,
+                        device=None):
+        """Average launch time (us, HIP events on this library's stream) of
+        dotl_mfma_ceiling_probe; flops per launch = workgroups * 4 * iters * 16
+        * 32768. Not in the reference's surface: a roofline measurement aid."""
+        import torch
+
+        dev = torch.device(device or "cuda")
+        sink = torch.zeros(1, dtype=torch.float32, device=dev)
+        stream = torch.cuda.current_stream(dev)
+
+        def launch():
+            self._check(self._lib.dotl_mfma_ceiling_probe(int(workgroups), int(iters),
+                                                          1 if random_operands else 0,
+                                                          sink.data_ptr(), self._stream(dev)))
+
+        for _ in range(warmup):
+            launch()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            launch()
+        b.record(stream)
+        b.synchronize()
+        return a.elapsed_time(b) * 1000.0 / reps
 
     def lds_dma_probe(self, src):
         """LDS contents after one wave's 16-byte-per-lane LDS-DMA load of src (256 int32)."""

@@ -83,6 +83,17 @@ int dotl_smoke_test_identity(const float* x, float* y, int64_t n, void* stream);
  * reference csrc/attention_wmma.cuh:798-828), run as a test, not at start-up. */
 int dotl_mfma_layout_probe(int32_t* out, void* stream);
 
+/* Sustained matrix-core rate, no reference counterpart (a measurement aid
+ * for the roofline): `workgroups` workgroups of 4 wavefronts, each wave
+ * `iters` rounds of 16 v_mfma_f32_32x32x16_f16 (32768 flops each) on
+ * register operands, random values when random_operands != 0 (as a GEMM's
+ * fragments are: the clock then drops under the matrix cores' power draw)
+ * else constants. Flops = workgroups * 4 * iters * 16 * 32768; the caller
+ * times the launch on `stream`. `sink` (one float, device) is never written
+ * in practice. */
+int dotl_mfma_ceiling_probe(int64_t workgroups, int32_t iters, int32_t random_operands, float* sink,
+                            void* stream);
+
 /*
  * LayerNorm over the last dimension, optionally fused with a residual add.
  * Replaces fused_add_layernorm / fused_layernorm

@@ -191,6 +191,16 @@ def test_bind_io_checks(lib):
     assert b"null slot" in lib.dotl_last_error()
 
 
+def test_mfma_ceiling_probe_checks(lib):
+    sink = ctypes.c_void_p(16)   # never dereferenced: every call below fails its checks first
+    assert lib.dotl_mfma_ceiling_probe(1, 1, 1, None, None) == -1
+    assert b"null sink" in lib.dotl_last_error()
+    assert lib.dotl_mfma_ceiling_probe(0, 1, 1, sink, None) == -1
+    assert lib.dotl_mfma_ceiling_probe(1, -1, 1, sink, None) == -1
+    assert lib.dotl_mfma_ceiling_probe(1, (1 << 20) + 1, 0, sink, None) == -1
+    assert b"workgroups" in lib.dotl_last_error()
+
+
 def test_ffn_block_checks(lib):
     def ffn(rows, D, F):
         return lib.dotl_ffn_block(*([None] * 12), rows, D, F, ctypes.c_double(1e-5), None)

@@ -24,6 +24,17 @@ def _t(a, dtype=torch.float32):
 
 # ---- MFMA accumulator layout ---------------------------------------------------
 
+def test_mfma_ceiling_probe_runs(kernels):
+    """The sustained-rate probe launches and times; the rate it implies stays
+    under the datasheet's 2.5 PFLOP/s (the probe counts its flops right)."""
+    wg, iters = 256, 16
+    flops = wg * 4 * iters * 16 * 32768
+    for rnd in (False, True):
+        us = kernels.mfma_ceiling_us(wg, iters, random_operands=rnd, reps=5, warmup=2)
+        assert us > 0
+        assert flops / (us * 1e-6) < 2.6e15
+
+
 def test_mfma_layout_probe(kernels):
     """The (row, col) each accumulator register holds, as the kernels assume it."""
     got = kernels.mfma_layout_probe().cpu().numpy()
