@@ -31,6 +31,24 @@ class AccuracyResult:
     optimized_at_worst: float
 
 
+def gate_ratio(reference, optimized, rtol: float = RTOL, atol: float = ATOL) -> float:
+    """How much of the rule's allowance the worst element uses: the maximum
+    over elements of min(err / atol, err / (rtol |ref|)). An element passes
+    iff its ratio is <= 1, so 1 - gate_ratio is the margin left. Non-finite
+    elements count as infinite. Not in the harness (its rule is pass/fail);
+    the parity tests use it to catch margin loss that max_abs would hide (an
+    element far above atol can pass on the relative arm)."""
+    ref = np.asarray(reference, dtype=np.float64)
+    opt = np.asarray(optimized, dtype=np.float64)
+    if ref.size == 0:
+        return 0.0
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        err = np.abs(opt - ref)
+        ratio = np.minimum(err / atol, err / (rtol * np.abs(ref)))
+    ratio = np.where(np.isfinite(ref) & np.isfinite(opt), ratio, np.inf)
+    return float(np.nanmax(ratio))
+
+
 def element_ok(reference, optimized, rtol: float = RTOL, atol: float = ATOL) -> np.ndarray:
     """Boolean array: which elements pass the rule."""
     ref = np.asarray(reference, dtype=np.float64)

@@ -18,13 +18,21 @@ import kernel_ext
 from layer_runner import TransformerConfig, build_model, to_device
 from optimized import config as ocfg
 from optimized import kernels as okernels
-from oracle.compare import compare_outputs
+from oracle.compare import compare_outputs, gate_ratio
 from oracle.inputs import CONFIGS, make_case, stack_layers as params_for
 from oracle.layer import reference_layer
 
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+# Margin regression bound: the share of the 2e-3 / 2% allowance the worst
+# element may use. Measured on MI355X with the default arithmetic: C4 0.76,
+# C5 0.77, C3 0.49, C2 0.52 (C4 seed 404: 0.77, C5 seed 505: 0.72); the tail
+# comes from the FFN GEMMs' fp16 operands (both in the split fp16x3
+# arithmetic, C4 drops to 0.09). A change that eats into the margin fails
+# here before it can fail the rule on another draw.
+MAX_GATE_RATIO = 0.85
 
 
 def _tcfg(cfg, batch=None, layers=1):
@@ -58,10 +66,12 @@ def test_layer_parity(kernels, name):
     torch.set_num_threads(max(1, min(16, os.cpu_count() or 1)))
     ref = reference_layer(x, mask, params, cfg).numpy()
     res = compare_outputs(ref, got)
+    gate = gate_ratio(ref, got)
     print(f"[layer parity] {name}: failed={res.failed_elements}/{res.total_elements} "
           f"max_abs={res.max_abs_error:.3e} mean_abs={res.mean_abs_error:.3e} "
-          f"worst={res.worst_index}", flush=True)
+          f"gate={gate:.3f} worst={res.worst_index}", flush=True)
     assert res.passed, res
+    assert gate <= MAX_GATE_RATIO, f"{name}: the worst element uses {gate:.3f} of the allowance"
     if mask is not None:
         assert np.all(got[~mask] == 0.0)
     fx = np.load(os.path.join(GOLDEN, f"rows_{name}.npz" if name != "C1" else "c1_layer.npz"),
@@ -90,9 +100,11 @@ def test_layer_parity_other_seeds(kernels, name, seed, batch):
     torch.set_num_threads(max(1, min(16, os.cpu_count() or 1)))
     ref = reference_layer(x, mask, params, cfg).numpy()
     res = compare_outputs(ref, got)
+    gate = gate_ratio(ref, got)
     print(f"[layer parity, seed {seed}] {name}: failed={res.failed_elements}/{res.total_elements} "
-          f"max_abs={res.max_abs_error:.3e}", flush=True)
+          f"max_abs={res.max_abs_error:.3e} gate={gate:.3f}", flush=True)
     assert res.passed, res
+    assert gate <= MAX_GATE_RATIO, f"{name} seed {seed}: the worst element uses {gate:.3f}"
     if mask is not None:
         assert np.all(got[~mask] == 0.0)
 

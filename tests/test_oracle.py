@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import brute
-from oracle.compare import compare_outputs, element_ok
+from oracle.compare import compare_outputs, element_ok, gate_ratio
 from oracle.inputs import (CONFIGS, LayerConfig, attention_useful_flops, gemm_flops, make_case,
                            stack_layers)
 from oracle.layer import (attention, gelu, layer_norm, linear, num_layers_of, reference_attention,
@@ -274,6 +274,25 @@ def test_compare_rule_is_or_not_isclose():
     assert np.isclose(opt[2], ref[2], rtol=0.02, atol=2e-3)
     r = compare_outputs(ref, opt)
     assert not r.passed and r.failed_elements == 1 and r.worst_index == (3,)
+
+
+def test_gate_ratio_is_the_rule_as_a_fraction():
+    """gate_ratio <= 1 exactly when every element passes, and it is the
+    larger of the two arms' slack, not max_abs: an element 50x over atol that
+    passes on the relative arm still reads below 1."""
+    ref = np.array([0.0, 1.0, 0.05, 100.0], dtype=np.float64)
+    opt = np.array([0.001, 1.01, 0.0505, 101.0], dtype=np.float64)
+    g = gate_ratio(ref, opt)
+    # per element: 0.5 (abs arm), 0.5 (both arms), 0.25 (abs), 0.5 (rel arm; 500x atol)
+    assert abs(g - 0.5) < 1e-12
+    assert element_ok(ref, opt).all()
+    rng = np.random.default_rng(7)
+    for _ in range(200):
+        r = rng.standard_normal(64) * rng.choice([1e-3, 1.0, 100.0])
+        o = r + rng.standard_normal(64) * rng.choice([1e-4, 1e-3, 1e-2])
+        assert (gate_ratio(r, o) <= 1.0) == bool(element_ok(r, o).all())
+    assert gate_ratio(ref, np.array([0.0, np.nan, 0.05, 100.0])) == np.inf
+    assert gate_ratio(np.zeros(0), np.zeros(0)) == 0.0
 
 
 def test_compare_nonfinite_fails():
