@@ -64,6 +64,14 @@ __device__ __forceinline__ float4 load_sum4(const TI* __restrict__ x, const TI* 
     return a;
 }
 
+// A value the compiler must treat as computed: narrowing it cannot be fused
+// into the multiply-add that produced it. Left free, the backend may turn
+// fp32 fma + fp16 conversion into one v_fma_mixlo_f16 (a single rounding to
+// fp16), which differs in the last fp16 bit from the fp32 result narrowed
+// with RNE -- the arithmetic the reference and every other kernel here use --
+// and whether it does depends on the surrounding code.
+__device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
+
 // Four normalised values to the normed output (split planes: hi, then lo
 // in the second [rows, D] plane).
 template <int NORMED>
@@ -71,6 +79,9 @@ __device__ __forceinline__ void store_normed4(void* __restrict__ normed, int64_t
                                              int64_t off, float4 o) {
     using TO = typename normed_type<NORMED>::type;
     TO* out = static_cast<TO*>(normed);
+    if constexpr (NORMED != DOTL_F32) {
+        opaque(o.x); opaque(o.y); opaque(o.z); opaque(o.w);
+    }
     if constexpr (NORMED == DOTL_F16X2) {
         half4 h, l;
         h[0] = to_half(o.x); h[1] = to_half(o.y); h[2] = to_half(o.z); h[3] = to_half(o.w);
@@ -88,6 +99,7 @@ __device__ __forceinline__ void store_normed1(void* __restrict__ normed, int64_t
                                               int64_t off, float o) {
     using TO = typename normed_type<NORMED>::type;
     TO* out = static_cast<TO*>(normed);
+    if constexpr (NORMED != DOTL_F32) opaque(o);
     if constexpr (NORMED == DOTL_F16X2) {
         const _Float16 h = to_half(o);
         out[off] = h;
@@ -100,7 +112,16 @@ __device__ __forceinline__ void store_normed1(void* __restrict__ normed, int64_t
 // Vector path: D % 4 == 0 and D <= 256 * CH. Chunk c of lane l covers row
 // elements [4 * (c * 64 + l), +4): 16-byte accesses for fp32, 8-byte for
 // the 16-bit types.
-template <typename TI, int CH, bool HAS_SUB, bool WRITE_XNEW, int NORMED>
+//
+// Each wave takes RPW rows per iteration: their row indices, then all their
+// loads, are issued before any reduction, and the RPW butterflies
+// interleave. Up to 1024 columns the weight and bias chunks are loaded once
+// per wave, not per row. Measured on MI355X at the configs' shapes: two rows
+// a wave at D <= 256 (C5's gathered norm1 54.5 -> 46.1 us, norm2 54.8 ->
+// 52.7, the scattering final norm 78.0 -> 68.9), one above; more rows lose
+// (fewer waves, and the last round of resident waves runs part-empty: four
+// at D = 256 gave 47.3 / 56.7 / 71.7 us, eight 51.1 / 68.9 / 91.9).
+template <typename TI, int CH, int RPW, bool HAS_SUB, bool WRITE_XNEW, int NORMED>
 __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     const TI* __restrict__ x, const TI* __restrict__ sub,
     const TI* __restrict__ w, const TI* __restrict__ b,
@@ -114,74 +135,111 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     const int nchunk = D >> 2;
     const float inv_d = 1.0f / static_cast<float>(D);
     const int64_t plane = rows * D;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
 
-    for (int64_t row = wave_global; row < rows; row += wave_stride) {
-        const int64_t base = row * D;   // output row
-        int64_t src = row_index ? static_cast<int64_t>(row_index[row]) : row;
-        if (src >= in_rows) src = -1;
-        if (src < 0) {
-            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    constexpr bool HOIST = CH <= 4;
+    float4 wv[HOIST ? CH : 1], bv[HOIST ? CH : 1];
+    if constexpr (HOIST) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int idx = c * 64 + lane;
+            wv[c] = idx < nchunk ? load4f(w + 4 * idx) : z;
+            bv[c] = idx < nchunk ? load4f(b + 4 * idx) : z;
+        }
+    }
+
+    for (int64_t g = wave_global; g * RPW < rows; g += wave_stride) {
+        const int64_t row0 = g * RPW;
+        // per row: its input row, -1 for a row of zeros, -2 past the end
+        int64_t src[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int64_t row = row0 + r;
+            int64_t s_ = -2;
+            if (row < rows) {
+                s_ = row_index ? static_cast<int64_t>(row_index[row]) : row;
+                if (s_ >= in_rows || s_ < 0) s_ = -1;
+            }
+            src[r] = s_;
+        }
+        float4 v[RPW][CH];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int idx = c * 64 + lane;
+                v[r][c] = (src[r] >= 0 && idx < nchunk)
+                              ? load_sum4<TI, HAS_SUB>(x, sub, src[r] * D + 4 * idx)
+                              : z;
+            }
+        float mean_est[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            float s_ = 0.f;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) s_ += (v[r][c].x + v[r][c].y) + (v[r][c].z + v[r][c].w);
+            mean_est[r] = s_;
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) mean_est[r] += __shfl_xor(mean_est[r], off, kWave);
+        float sd[RPW], sd2[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            mean_est[r] *= inv_d;
+            sd[r] = 0.f;
+            sd2[r] = 0.f;
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
                 const int idx = c * 64 + lane;
                 if (idx < nchunk) {
-                    if constexpr (WRITE_XNEW) store4f(x_new + base + 4 * idx, z);
-                    store_normed4<NORMED>(normed, plane, base + 4 * idx, z);
+                    const float d0 = v[r][c].x - mean_est[r], d1 = v[r][c].y - mean_est[r];
+                    const float d2 = v[r][c].z - mean_est[r], d3 = v[r][c].w - mean_est[r];
+                    sd[r] += (d0 + d1) + (d2 + d3);
+                    sd2[r] += ln_sq4(d0, d1, d2, d3);
                 }
             }
-            continue;
         }
-        const int64_t ibase = src * D;  // input row
-        float4 v[CH];
-        float s = 0.f;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int idx = c * 64 + lane;
-            if (idx < nchunk) {
-                v[c] = load_sum4<TI, HAS_SUB>(x, sub, ibase + 4 * idx);
-            } else {
-                v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                sd[r] += __shfl_xor(sd[r], off, kWave);
+                sd2[r] += __shfl_xor(sd2[r], off, kWave);
             }
-            s += (v[c].x + v[c].y) + (v[c].z + v[c].w);
-        }
-        const float mean_est = wave_sum(s) * inv_d;
-
-        float sd = 0.f, sd2 = 0.f;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int idx = c * 64 + lane;
-            if (idx < nchunk) {
-                const float d0 = v[c].x - mean_est, d1 = v[c].y - mean_est;
-                const float d2 = v[c].z - mean_est, d3 = v[c].w - mean_est;
-                sd += (d0 + d1) + (d2 + d3);
-                sd2 += ln_sq4(d0, d1, d2, d3);
-            }
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            sd += __shfl_xor(sd, off, kWave);
-            sd2 += __shfl_xor(sd2, off, kWave);
-        }
-        const float delta = sd * inv_d;
-        const float var = ln_var(sd2, delta, inv_d);
-        const float rstd = 1.0f / sqrtf(var + eps);
 
         // x - mean as (x - m) - delta: x - m is exact (both near the mean),
         // whereas forming m + delta first would round the mean to ulp(mean).
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int idx = c * 64 + lane;
-            if (idx < nchunk) {
-                const int col = 4 * idx;
-                if constexpr (WRITE_XNEW) store4f(x_new + base + col, v[c]);
-                const float4 ww = load4f(w + col);
-                const float4 bb = load4f(b + col);
-                float4 o;
-                o.x = ln_out(v[c].x, mean_est, delta, rstd, ww.x, bb.x);
-                o.y = ln_out(v[c].y, mean_est, delta, rstd, ww.y, bb.y);
-                o.z = ln_out(v[c].z, mean_est, delta, rstd, ww.z, bb.z);
-                o.w = ln_out(v[c].w, mean_est, delta, rstd, ww.w, bb.w);
-                store_normed4<NORMED>(normed, plane, base + col, o);
+        for (int r = 0; r < RPW; ++r) {
+            if (src[r] == -2) continue;   // wave-uniform
+            const int64_t base = (row0 + r) * D;
+            const bool zero = src[r] < 0;
+            const float delta = sd[r] * inv_d;
+            const float var = ln_var(sd2[r], delta, inv_d);
+            const float rstd = 1.0f / sqrtf(var + eps);
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int idx = c * 64 + lane;
+                if (idx < nchunk) {
+                    const int col = 4 * idx;
+                    if constexpr (WRITE_XNEW) store4f(x_new + base + col, zero ? z : v[r][c]);
+                    float4 ww, bb;
+                    if constexpr (HOIST) {
+                        ww = wv[c];
+                        bb = bv[c];
+                    } else {
+                        ww = load4f(w + col);
+                        bb = load4f(b + col);
+                    }
+                    float4 o;
+                    o.x = ln_out(v[r][c].x, mean_est[r], delta, rstd, ww.x, bb.x);
+                    o.y = ln_out(v[r][c].y, mean_est[r], delta, rstd, ww.y, bb.y);
+                    o.z = ln_out(v[r][c].z, mean_est[r], delta, rstd, ww.z, bb.z);
+                    o.w = ln_out(v[r][c].w, mean_est[r], delta, rstd, ww.w, bb.w);
+                    store_normed4<NORMED>(normed, plane, base + col, zero ? z : o);
+                }
             }
         }
     }
@@ -291,7 +349,9 @@ unsigned grid_for(int64_t rows) {
 
 template <typename TI, int CH, bool HAS_SUB, bool WX, int NO>
 void launch_vec(const LnArgs& a) {
-    hipLaunchKernelGGL((layernorm_vec_kernel<TI, CH, HAS_SUB, WX, NO>), dim3(grid_for(a.rows)),
+    constexpr int RPW = CH <= 1 ? 2 : 1;
+    hipLaunchKernelGGL((layernorm_vec_kernel<TI, CH, RPW, HAS_SUB, WX, NO>),
+                       dim3(grid_for((a.rows + RPW - 1) / RPW)),
                        dim3(256), 0, a.stream, static_cast<const TI*>(a.x),
                        static_cast<const TI*>(a.sub), static_cast<const TI*>(a.w),
                        static_cast<const TI*>(a.b), static_cast<TI*>(a.x_new), a.normed,
