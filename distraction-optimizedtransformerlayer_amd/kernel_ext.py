@@ -764,7 +764,7 @@ class Kernels:
         F = int(ffn_in_w.shape[0])
         if (tuple(ffn_in_w.shape) != (F, D) or tuple(ffn_out_w.shape) != (D, F)):
             raise RuntimeError(f"{who}: weight shapes disagree with d_model={D} ffn_dim={F}")
-        if D > 128 or F > 128 or D % 8 or F % 8:
+        if D > 128 or F > 512 or D % 8 or F % 8:
             return []
         xc, ac = x.contiguous(), attn_out.contiguous()
         rows = xc.numel() // D

@@ -437,7 +437,7 @@ def _ffn_block_eligible(x, ffn_in, ffn_out) -> bool:
     d_model, d_ff = x.shape[-1], ffn_in.weight.shape[0]
     if config.FFN_BLOCK != "force" and d_model > config._FFN_BLOCK_MAX_D:
         return False
-    return d_model <= 128 and d_ff <= 128 and d_model % 8 == 0 and d_ff % 8 == 0
+    return d_model <= 128 and d_ff <= 512 and d_model % 8 == 0 and d_ff % 8 == 0
 
 
 def _ffn_block(x, attn_out, norm1, ffn_in, ffn_out, norm2):

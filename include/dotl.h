@@ -312,9 +312,10 @@ int dotl_attention_split_plan(int B, int H, int S, int head_dim, int is_causal, 
  * weights, RNE); biases and LayerNorm parameters fp32. The arithmetic is the
  * unfused chain's (fp16 operands, fp32 accumulation, h rounded to fp16), so
  * the outputs equal that chain's bit for bit.
- * Covers D and F up to 128 in multiples of 8 (the reference instantiates
- * D == F in {16, 32, 48, 64, 128}); other widths return DOTL_DECLINED and the
- * caller runs the unfused chain, as the reference's empty-list decline.
+ * Covers D up to 128 and F up to 512, multiples of 8 (the reference
+ * instantiates D == F in {16, 32, 48, 64, 128}; F up to 512 adds the 4x FFN
+ * of d_model 128); other widths return DOTL_DECLINED and the caller runs the
+ * unfused chain, as the reference's empty-list decline.
  * Tensors 16-byte aligned.
  */
 int dotl_ffn_block(const float* x, const float* attn_out, const float* norm1_w,

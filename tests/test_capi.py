@@ -207,7 +207,7 @@ def test_ffn_block_checks(lib):
 
     # widths past 128, or not multiples of 8: declined, the caller runs the chain
     assert ffn(16, 256, 256) == 1
-    assert ffn(16, 128, 512) == 1
+    assert ffn(16, 128, 640) == 1
     assert ffn(16, 60, 64) == 1
     assert b"not covered" in lib.dotl_last_error()
     # covered widths: an empty problem launches nothing; null tensors are an error

@@ -57,7 +57,9 @@ def _oracle(x, a, p):
     return x2, ln(x2, d["w2"], d["b2"])
 
 
-SHAPES = [(16, 16), (32, 32), (48, 48), (64, 64), (128, 128), (40, 96), (128, 24), (8, 8)]
+SHAPES = [(16, 16), (32, 32), (48, 48), (64, 64), (128, 128), (40, 96), (128, 24), (8, 8),
+          # d_ff above 128: the padded 256 and 512 instances (C1 is 128 x 512)
+          (128, 512), (64, 256), (128, 384), (96, 200)]
 
 
 @pytest.mark.parametrize("rows", [1, 64, 130, 1000])
@@ -91,6 +93,10 @@ def test_fused_block_batched_shape_and_declines(kernels):
     # widths outside the kernel: the empty-list decline
     pw = _params(256, 256, 2)
     xw = torch.randn(4, 256, device=DEV)
+    assert kernels.fused_ffn_block(xw, xw, pw["w1"], pw["b1"], pw["win"], pw["bin"], pw["wout"],
+                                   pw["bout"], pw["w2"], pw["b2"], EPS) == []
+    pw = _params(128, 640, 3)
+    xw = torch.randn(4, 128, device=DEV)
     assert kernels.fused_ffn_block(xw, xw, pw["w1"], pw["b1"], pw["win"], pw["bin"], pw["wout"],
                                    pw["bout"], pw["w2"], pw["b2"], EPS) == []
     with pytest.raises(RuntimeError, match="must match"):
