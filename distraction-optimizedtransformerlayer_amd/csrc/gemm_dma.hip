@@ -9,11 +9,12 @@ using gemm_dma::dispatch_tile;
 
 // Tile choice, from sweeps of every GEMM of the five layer configs on MI355X
 // (passes = planes multiplied: 1 + split x + split W):
-//   * one pass: 256x256 with 8 waves for wide products (N >= 4096, K >= 1024);
-//     256x256 with 128-byte K rows for K >= 2048 once that gives a
-//     workgroup per CU; else the 128x128 two-stage tile (two workgroups a
-//     CU) when it fills the CUs four times over, or at short K; else
-//     128x64, then 64x64;
+//   * one pass: 256x256 with 8 waves (tile 15) for K >= 1024 once that
+//     gives about a workgroup per CU, or 256x128 with 8 waves (17) where
+//     that fills the last wave of workgroups better; else the 128x128
+//     two-stage tile (12, two workgroups a CU) when it fills the CUs four
+//     times over, or at K <= 1024; else the 128x64 three-stage tile (13),
+//     then the 64x64 one (8);
 //   * split passes: two passes at K <= 512 on the 192x128 tile (C2's QKV,
 //     M = 3487: 228 tiles in one wave instead of a short second wave of
 //     128-row tiles, 20.5 vs 23.8 us; C5's: 125.8 vs 130.9 us; at K = 1024
@@ -25,8 +26,15 @@ int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
         // large products: the 8-wave 256x256 tile (two waves a SIMD hide
         // each other's waits) with the LDS-staged epilogue, measured on
         // MI355X against the 4-wave one: C4 QKV 181 vs 202 us, ffn_in 275 vs
-        // 292, ffn_out (+ residual) 241 vs 242, out_proj 78 vs 80
-        if (K >= 1024 && tiles(256, 256) >= 240) return 15;
+        // 292, ffn_out (+ residual) 241 vs 242, out_proj 78 vs 80.
+        // When its tiles leave the last of the waves of 256 workgroups (one
+        // a CU) mostly empty, the 256x128 three-stage tile instead: C5's
+        // ffn_out (N = 256, 333 tiles: 65% of two waves; 256x128: 666
+        // tiles, 87% of three) 83 vs 93 us.
+        if (K >= 1024 && tiles(256, 256) >= 240) {
+            auto fill = [](int64_t t) { return static_cast<double>(t) / (((t + 255) / 256) * 256); };
+            return fill(tiles(256, 128)) > fill(tiles(256, 256)) + 0.1 ? 17 : 15;
+        }
         if (tiles(128, 128) >= 960) return 12;
         if (tiles(128, 128) >= 240 && K <= 1024) return 12;
         if (tiles(128, 64) >= 200) return 13;

@@ -430,40 +430,50 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
     const bool vec_ok = (N & 3) == 0;
     // The direct epilogue (each lane stores its own runs of 4 columns) for a
     // GELU with a 16-bit output: there the staged one measured no better
-    // (C4 ffn_in shape 288 us either way on the 8-wave tile) and worse on
+    // (C4 ffn_in shape on the 8-wave tile, both with the full-tile paths
+    // below: 266-271 us direct, 272-274 staged; C5's equal) and worse on
     // the 4-wave ones, whose waves have no partner to overlap the transpose.
     constexpr bool STAGED = !(ACT == DOTL_ACT_GELU && OUTT != DOTL_F32);
     if constexpr (!STAGED) {
+        // A tile wholly inside C stores without per-row or per-column tests
+        // (the same reason as the staged rounds below).
+        auto direct = [&](auto fullc) {
+            constexpr bool FULL = decltype(fullc)::value;
 #pragma unroll
-        for (int i = 0; i < G::TM; ++i) {
-            const int64_t row = g.m0 + g.wm * G::WM + i * 32 + g.lr;
-            if (row >= M) continue;
+            for (int i = 0; i < G::TM; ++i) {
+                const int64_t row = g.m0 + g.wm * G::WM + i * 32 + g.lr;
+                if (!FULL && row >= M) continue;
 #pragma unroll
-            for (int j = 0; j < G::TN; ++j) {
+                for (int j = 0; j < G::TN; ++j) {
 #pragma unroll
-                for (int grp = 0; grp < 4; ++grp) {
-                    const int cl = g.wn * G::WN + j * 32 + 8 * grp + 4 * g.lg;  // tile-local column
-                    const int64_t col = g.n0 + cl;
-                    float v[4];
+                    for (int grp = 0; grp < 4; ++grp) {
+                        const int cl = g.wn * G::WN + j * 32 + 8 * grp + 4 * g.lg;  // tile-local column
+                        const int64_t col = g.n0 + cl;
+                        float v[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        float a = g.acc[i][j][4 * grp + e];
-                        if constexpr (G::SPLIT) a += g.acc2[i][j][4 * grp + e] * kLoUnscale;
-                        a += sbias[cl + e];
-                        if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
-                        v[e] = a;
-                    }
-                    TO* crow = static_cast<TO*>(C) + row * N;
-                    if (vec_ok && col + 4 <= N) {
-                        store4f(crow + col, make_float4(v[0], v[1], v[2], v[3]));
-                    } else {
+                        for (int e = 0; e < 4; ++e) {
+                            float a = g.acc[i][j][4 * grp + e];
+                            if constexpr (G::SPLIT) a += g.acc2[i][j][4 * grp + e] * kLoUnscale;
+                            a += sbias[cl + e];
+                            if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
+                            v[e] = a;
+                        }
+                        TO* crow = static_cast<TO*>(C) + row * N;
+                        if (FULL || (vec_ok && col + 4 <= N)) {
+                            store4f(crow + col, make_float4(v[0], v[1], v[2], v[3]));
+                        } else {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            if (col + e < N) crow[col + e] = from_f32<TO>(v[e]);
+                            for (int e = 0; e < 4; ++e)
+                                if (col + e < N) crow[col + e] = from_f32<TO>(v[e]);
+                        }
                     }
                 }
             }
-        }
+        };
+        if (vec_ok && g.m0 + BM <= M && g.n0 + BN <= N)
+            direct(std::integral_constant<bool, true>{});
+        else
+            direct(std::integral_constant<bool, false>{});
         return;
     } else {
     constexpr int BUF_BYTES = SZ * 2;
@@ -487,108 +497,124 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
         return reinterpret_cast<float*>(p);
     };
     stage_barrier();   // every wave is done reading the stages
-    static_for<0, ROUNDS>([&](auto qq) {
-        constexpr int q = decltype(qq)::value;
-        constexpr int r_lo = q * RR;
-        constexpr int r_hi = (q + 1) * RR < BM ? (q + 1) * RR : BM;
-        constexpr int CHUNKS = (r_hi - r_lo) * CPR;
-        static_assert(CHUNKS % THREADS == 0, "round chunks");
-        constexpr int PER_T = CHUNKS / THREADS;
-        // The round's residual, loaded first: its HBM latency then runs
-        // under the LDS writes and the barrier instead of stalling the
-        // store loop once per batch.
-        float4 res[OUTT == DOTL_F32 ? PER_T : 1];
-        if constexpr (OUTT == DOTL_F32) {
-            if (R != nullptr) {
+    // A tile wholly inside C (every tile but the right and bottom edges)
+    // takes a copy of the rounds with no per-row or per-column tests: its
+    // residual loads and stores are then single 16-byte accesses in a
+    // straight line, so the compiler can count them and wait only for what
+    // each chunk needs instead of draining every store before the next.
+    auto rounds = [&](auto fullc) {
+        constexpr bool FULL = decltype(fullc)::value;
+        static_for<0, ROUNDS>([&](auto qq) {
+            constexpr int q = decltype(qq)::value;
+            constexpr int r_lo = q * RR;
+            constexpr int r_hi = (q + 1) * RR < BM ? (q + 1) * RR : BM;
+            constexpr int CHUNKS = (r_hi - r_lo) * CPR;
+            static_assert(CHUNKS % THREADS == 0, "round chunks");
+            constexpr int PER_T = CHUNKS / THREADS;
+            // The round's residual, loaded first: its HBM latency then runs
+            // under the LDS writes and the barrier instead of stalling the
+            // store loop once per batch.
+            float4 res[OUTT == DOTL_F32 ? PER_T : 1];
+            if constexpr (OUTT == DOTL_F32) {
+                if (R != nullptr) {
 #pragma unroll
-                for (int u = 0; u < PER_T; ++u) {
-                    const int c = threadIdx.x + u * THREADS;
-                    const int64_t row = g.m0 + r_lo + c / CPR;
-                    const int64_t col = g.n0 + (c % CPR) * 4;
-                    res[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (row < M) {
+                    for (int u = 0; u < PER_T; ++u) {
+                        const int c = threadIdx.x + u * THREADS;
+                        const int64_t row = g.m0 + r_lo + c / CPR;
+                        const int64_t col = g.n0 + (c % CPR) * 4;
                         const float* rrow = R + row * N + col;
-                        if (vec_ok && col + 4 <= N) {
+                        if constexpr (FULL) {
                             res[u] = *reinterpret_cast<const float4*>(rrow);
-                        } else {
-                            if (col + 0 < N) res[u].x = rrow[0];
-                            if (col + 1 < N) res[u].y = rrow[1];
-                            if (col + 2 < N) res[u].z = rrow[2];
-                            if (col + 3 < N) res[u].w = rrow[3];
+                            continue;
+                        }
+                        res[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+                        if (row < M) {
+                            if (vec_ok && col + 4 <= N) {
+                                res[u] = *reinterpret_cast<const float4*>(rrow);
+                            } else {
+                                if (col + 0 < N) res[u].x = rrow[0];
+                                if (col + 1 < N) res[u].y = rrow[1];
+                                if (col + 2 < N) res[u].z = rrow[2];
+                                if (col + 3 < N) res[u].w = rrow[3];
+                            }
                         }
                     }
                 }
             }
-        }
-        if constexpr (q > 0) stage_barrier();   // the previous round's reads are done
-        // write: this wave's 32-row groups that fall in the round
+            if constexpr (q > 0) stage_barrier();   // the previous round's reads are done
+            // write: this wave's 32-row groups that fall in the round
 #pragma unroll
-        for (int i = 0; i < G::TM; ++i) {
-            const int gb = g.wm * G::WM + i * 32;   // wave-uniform
-            if (gb < r_lo || gb >= r_hi) continue;
-            const int b = (gb - r_lo) / RPB;
-            const int rb = (gb - r_lo) % RPB + g.lr;
-            float* base = buf(b) + rb * BN;
+            for (int i = 0; i < G::TM; ++i) {
+                const int gb = g.wm * G::WM + i * 32;   // wave-uniform
+                if (gb < r_lo || gb >= r_hi) continue;
+                const int b = (gb - r_lo) / RPB;
+                const int rb = (gb - r_lo) % RPB + g.lr;
+                float* base = buf(b) + rb * BN;
 #pragma unroll
-            for (int j = 0; j < G::TN; ++j) {
+                for (int j = 0; j < G::TN; ++j) {
 #pragma unroll
-                for (int grp = 0; grp < 4; ++grp) {
-                    const int chunk = (g.wn * G::WN + j * 32 + 8 * grp) / 4 + g.lg;
-                    float4 v;
-                    v.x = g.acc[i][j][4 * grp + 0];
-                    v.y = g.acc[i][j][4 * grp + 1];
-                    v.z = g.acc[i][j][4 * grp + 2];
-                    v.w = g.acc[i][j][4 * grp + 3];
-                    if constexpr (G::SPLIT) {
-                        v.x += g.acc2[i][j][4 * grp + 0] * kLoUnscale;
-                        v.y += g.acc2[i][j][4 * grp + 1] * kLoUnscale;
-                        v.z += g.acc2[i][j][4 * grp + 2] * kLoUnscale;
-                        v.w += g.acc2[i][j][4 * grp + 3] * kLoUnscale;
+                    for (int grp = 0; grp < 4; ++grp) {
+                        const int chunk = (g.wn * G::WN + j * 32 + 8 * grp) / 4 + g.lg;
+                        float4 v;
+                        v.x = g.acc[i][j][4 * grp + 0];
+                        v.y = g.acc[i][j][4 * grp + 1];
+                        v.z = g.acc[i][j][4 * grp + 2];
+                        v.w = g.acc[i][j][4 * grp + 3];
+                        if constexpr (G::SPLIT) {
+                            v.x += g.acc2[i][j][4 * grp + 0] * kLoUnscale;
+                            v.y += g.acc2[i][j][4 * grp + 1] * kLoUnscale;
+                            v.z += g.acc2[i][j][4 * grp + 2] * kLoUnscale;
+                            v.w += g.acc2[i][j][4 * grp + 3] * kLoUnscale;
+                        }
+                        *reinterpret_cast<float4*>(base + ((chunk ^ (rb & 15)) * 4)) = v;
                     }
-                    *reinterpret_cast<float4*>(base + ((chunk ^ (rb & 15)) * 4)) = v;
                 }
             }
-        }
-        stage_barrier();
-        // read + store: row-contiguous chunks of rows [r_lo, r_hi)
+            stage_barrier();
+            // read + store: row-contiguous chunks of rows [r_lo, r_hi)
 #pragma unroll
-        for (int u = 0; u < PER_T; ++u) {
-            const int c = threadIdx.x + u * THREADS;
-            const int rl = c / CPR;                 // row within the round
-            const int cc = c % CPR;                 // logical chunk
-            const int b = rl / RPB;
-            const int rb = rl % RPB;
-            const int64_t row = g.m0 + r_lo + rl;
-            const int cl = cc * 4;                  // tile-local column
-            const int64_t col = g.n0 + cl;
-            if (row >= M) continue;
-            const float4 a4 =
-                *reinterpret_cast<const float4*>(buf(b) + rb * BN + ((cc ^ (rb & 15)) * 4));
-            float v[4] = {a4.x, a4.y, a4.z, a4.w};
+            for (int u = 0; u < PER_T; ++u) {
+                const int c = threadIdx.x + u * THREADS;
+                const int rl = c / CPR;                 // row within the round
+                const int cc = c % CPR;                 // logical chunk
+                const int b = rl / RPB;
+                const int rb = rl % RPB;
+                const int64_t row = g.m0 + r_lo + rl;
+                const int cl = cc * 4;                  // tile-local column
+                const int64_t col = g.n0 + cl;
+                if (!FULL && row >= M) continue;
+                const float4 a4 =
+                    *reinterpret_cast<const float4*>(buf(b) + rb * BN + ((cc ^ (rb & 15)) * 4));
+                float v[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float a = v[e] + sbias[cl + e];
-                if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
-                v[e] = a;
-            }
-            if constexpr (OUTT == DOTL_F32) {
-                // residual stream: out = R + act(x W^T + b), the add the
-                // following LayerNorm would otherwise do (same fp32 sum)
-                if (R != nullptr) {
-                    v[0] = res[u].x + v[0]; v[1] = res[u].y + v[1];
-                    v[2] = res[u].z + v[2]; v[3] = res[u].w + v[3];
+                for (int e = 0; e < 4; ++e) {
+                    float a = v[e] + sbias[cl + e];
+                    if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
+                    v[e] = a;
+                }
+                if constexpr (OUTT == DOTL_F32) {
+                    // residual stream: out = R + act(x W^T + b), the add the
+                    // following LayerNorm would otherwise do (same fp32 sum)
+                    if (R != nullptr) {
+                        v[0] = res[u].x + v[0]; v[1] = res[u].y + v[1];
+                        v[2] = res[u].z + v[2]; v[3] = res[u].w + v[3];
+                    }
+                }
+                TO* crow = static_cast<TO*>(C) + row * N;
+                if (FULL || (vec_ok && col + 4 <= N)) {
+                    store4f(crow + col, make_float4(v[0], v[1], v[2], v[3]));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (col + e < N) crow[col + e] = from_f32<TO>(v[e]);
                 }
             }
-            TO* crow = static_cast<TO*>(C) + row * N;
-            if (vec_ok && col + 4 <= N) {
-                store4f(crow + col, make_float4(v[0], v[1], v[2], v[3]));
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (col + e < N) crow[col + e] = from_f32<TO>(v[e]);
-            }
-        }
-    });
+        });
+    };
+    if (vec_ok && g.m0 + BM <= M && g.n0 + BN <= N)
+        rounds(std::integral_constant<bool, true>{});
+    else
+        rounds(std::integral_constant<bool, false>{});
     }
 }
 

@@ -482,7 +482,7 @@ def test_gemm_dma_split_planes(kernels, M, N, K, tile, act):
 
 
 @pytest.mark.parametrize("M,N,K", DMA_SHAPES)
-@pytest.mark.parametrize("tile", [-1, 3, 5, 9, 10, 12, 13])
+@pytest.mark.parametrize("tile", [-1, 3, 5, 9, 10, 12, 13, 15, 16, 17])
 def test_gemm_residual_epilogue(kernels, M, N, K, tile):
     """linear_bias(residual=R) = R + linear_bias() bit for bit: the epilogue adds
     the same fp32 values in the same order as a separate add would."""
