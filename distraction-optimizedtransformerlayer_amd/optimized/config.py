@@ -149,12 +149,12 @@ ROW_PACKING = "auto"
 # and ffn_out write h1 + ffn (the same fp32 sums, bit-identical outputs), so
 # the LayerNorms after them read one tensor and write only the normalised
 # one; "off" keeps the reference's add+LayerNorm kernels. "auto" applies
-# from d_model _RESIDUAL_EPILOGUE_MIN_D: the epilogue's residual reads cost
-# more than the LayerNorm traffic they save when K is short. Same-box A/B
-# (layer µs, on / off): C3 307 / 312, C4 1446 / 1460; C1 42.3 / 40.7,
-# C2 120.7 / 119.2, C5 627 / 622.
+# from d_model _RESIDUAL_EPILOGUE_MIN_D. Since tiles wholly inside the output
+# load the residual and store in straight lines it pays at every config;
+# same-box A/B (layer µs, min 1024 / 0, i.e. off / on below C3): C1 36.6 /
+# 35.4, C2 96.0 / 93.6, C3 268.6 / 268.7, C5 574 / 544.
 RESIDUAL_EPILOGUE = "auto"
-_RESIDUAL_EPILOGUE_MIN_D = 1024
+_RESIDUAL_EPILOGUE_MIN_D = 0
 
 # Arithmetic of a model with more than one block. Each block's fp16 operand
 # roundings add to the residual stream the next block reads, so the error at

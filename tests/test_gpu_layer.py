@@ -300,7 +300,7 @@ def test_residual_epilogue_is_bit_identical(kernels, name):
     saved = (ocfg.RESIDUAL_EPILOGUE, ocfg._RESIDUAL_EPILOGUE_MIN_D)
     try:
         outs = {}
-        ocfg._RESIDUAL_EPILOGUE_MIN_D = 0   # these widths sit below the speed threshold
+        ocfg._RESIDUAL_EPILOGUE_MIN_D = 0   # every width, whatever the default threshold
         for mode in ("auto", "off"):
             ocfg.RESIDUAL_EPILOGUE = mode
             okernels.fallback_counts.clear()
