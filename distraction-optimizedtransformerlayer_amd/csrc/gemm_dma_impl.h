@@ -65,6 +65,12 @@ namespace gemm_dma {
 
 constexpr int kThreads = 256;
 constexpr int kXcds = 8;
+// Share of the last k step's MFMAs a tile defers past the next barrier, in
+// eighths (DmaGemm::compute). Same-box A/B on MI355X, none / half / all
+// (bit-identical outputs): C4 QKV 188 / 180 / 174 us, ffn_in 263 / 257 /
+// 255, ffn_out + residual 240 / 238 / 236, C3 split QKV 64 / 61 / 61, C5
+// ffn_in 118 / 114 / 110.
+constexpr int kDeferEighths = 8;
 constexpr int kGroupM = 8;
 
 __device__ __forceinline__ void tile_of(int64_t id, int64_t nm, int64_t nn, int64_t& mt,
@@ -191,42 +197,78 @@ struct DmaGemm {
     }
 
     // Multiply the tile in `stage`; if `more`, issue tile kt_next into
-    // `next` meanwhile. Two schedules, both measured on MI355X:
+    // `next` meanwhile. Three schedules, all measured on MI355X:
     //   * with two stages the next tile's DMAs all go out during the first
-    //     two 16-deep k steps, one after an MFMA (the vector-memory issue
-    //     stalls while the CU's load queue is full; behind an MFMA the stall
-    //     is hidden), so the stage's round trip (~1.3 us for 64 KiB, one
-    //     stage in flight a CU) runs under the tile's remaining MFMAs.
-    //     Spread evenly over the tile, the last slice was issued at its end
-    //     and the barrier waited out its full latency;
+    //     two 16-deep k steps' worth of MFMAs, one after an MFMA (the
+    //     vector-memory issue stalls while the CU's load queue is full;
+    //     behind an MFMA the stall is hidden), so the stage's round trip
+    //     (~1.3 us for 64 KiB, one stage in flight a CU) runs under the
+    //     tile's remaining MFMAs. Spread evenly over the tile, the last slice
+    //     was issued at its end and the barrier waited out its full latency;
     //   * the fragments of k step ks + 1 are read from LDS before the MFMAs
-    //     of step ks are issued, so their latency too runs under MFMAs.
-    __device__ __forceinline__ void load_frags(const _Float16* stage, int ks, half8 (&a)[TM],
-                                               half8 (&b)[TN]) const {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) a[i] = frag(stage + L::A_ROW * BK, wm * WM + i * 32 + lr, ks);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) b[j] = frag(stage + L::W_ROW * BK, wn * WN + j * 32 + lr, ks);
+    //     of step ks are issued, so their latency too runs under MFMAs;
+    //   * DEFER of the last k step's PER MFMAs (one per accumulator) are
+    //     issued after the next tile's barrier, from fragments already in
+    //     registers: they keep the matrix core busy while that tile's first
+    //     fragment reads are in flight, a latency every wave otherwise waited
+    //     out with the core idle at each tile boundary (the ones not deferred
+    //     would cover the waves' skew in reaching the barrier instead; all
+    //     deferred measured best).
+    static constexpr int PER = TM * TN;
+    static constexpr int DEFER = PER * kDeferEighths / 8;
+    static_assert(KS % 2 == 0, "the deferred fragments sit in register set 1");
+    half8 fa[2][TM], fb[2][TN];
+
+    // The deferred MFMAs of the previous tile (all of them when it is the last).
+    template <int LO, int HI>
+    __device__ __forceinline__ void deferred_mma() {
+        static_for<LO, HI>([&](auto mm) {
+            constexpr int m = PER - DEFER + decltype(mm)::value;
+            constexpr int i = m / TN, j = m % TN;
+            acc[i][j] = mma(fb[1][j], fa[1][i], acc[i][j]);
+        });
     }
+    __device__ __forceinline__ void finish() { deferred_mma<0, DEFER>(); }
 
     __device__ __forceinline__ void compute(const _Float16* stage, _Float16* next, int64_t kt_next,
-                                            bool more) {
-        // k steps the DMAs are spread over: the first two with two stages
-        // (the next barrier waits for them; on MI355X two beat one by 1-4%
-        // and all four lose 3-5%); with more stages each tile has NS - 2
-        // further tiles' MFMAs to land, and an even spread issues more gently.
-        constexpr int ISSUE_KS = NS == 2 ? (KS < 2 ? KS : 2) : KS;
-        constexpr int PER = TM * TN;                    // MFMAs a k step
-        constexpr int SLOTS = ISSUE_KS * PER;
+                                            bool more, bool pend) {
+        // MFMA rounds the DMAs are spread over: the first two k steps' worth
+        // with two stages (the next barrier waits for them; on MI355X two
+        // beat one by 1-4% and all four lose 3-5%); with more stages each
+        // tile has NS - 2 further tiles' MFMAs to land, and an even spread
+        // over the whole tile issues more gently.
+        constexpr int ISSUE = (NS == 2 ? (KS < 2 ? KS : 2) : KS) * PER;
         constexpr int NF = TM + TN;                     // fragment reads a k step
         constexpr int ROUNDS = PER > NF ? PER : NF;
-        half8 fa[2][TM], fb[2][TN];
-        load_frags(stage, 0, fa[0], fb[0]);
+        auto dma_slot = [&](auto rr) {
+            constexpr int r = decltype(rr)::value;      // MFMA round within the tile
+            if constexpr (r < ISSUE) {
+                if (more) issue_range<r * NDMA / ISSUE, (r + 1) * NDMA / ISSUE>(next, kt_next);
+            }
+        };
+        // Phase 0: the previous tile's deferred MFMAs, this tile's first
+        // fragment reads, the first DMA slices.
+        static_for<0, (DEFER > NF ? DEFER : NF)>([&](auto mm) {
+            constexpr int m = decltype(mm)::value;
+            if constexpr (m < DEFER) {
+                if (pend) deferred_mma<m, m + 1>();
+                dma_slot(std::integral_constant<int, m>{});
+            }
+            if constexpr (m < NF) {
+                if constexpr (m < TM)
+                    fa[0][m] = frag(stage + L::A_ROW * BK, wm * WM + m * 32 + lr, 0);
+                else
+                    fb[0][m - TM] = frag(stage + L::W_ROW * BK, wn * WN + (m - TM) * 32 + lr, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
         static_for<0, KS>([&](auto kk) {
             constexpr int ks = decltype(kk)::value;
             constexpr int cur = ks & 1;
             half8 (&a)[TM] = fa[cur];
             half8 (&b)[TN] = fb[cur];
+            // MFMAs of this step: all of them, or the last step's undeferred.
+            constexpr int NM = ks + 1 < KS ? PER : PER - DEFER;
             // Round m: MFMA m of this step, fragment read m of the next step,
             // DMA slice m. The scheduling barrier after each round keeps the
             // compiler from regrouping them: left free it sank the reads of
@@ -234,11 +276,12 @@ struct DmaGemm {
             // and every step then began by waiting out a full LDS read
             // latency with the matrix core idle -- the loop ran at ~55% of
             // the MFMA rate with no global traffic at all.
-            static_for<0, ROUNDS>([&](auto mm) {
+            static_for<0, (NM > NF ? NM : NF)>([&](auto mm) {
                 constexpr int m = decltype(mm)::value;
-                if constexpr (m < PER) {
+                if constexpr (m < NM) {
                     constexpr int i = m / TN, j = m % TN;
                     acc[i][j] = mma(b[j], a[i], acc[i][j]);
+                    dma_slot(std::integral_constant<int, DEFER + ks * PER + m>{});
                 }
                 if constexpr (ks + 1 < KS && m < NF) {
                     if constexpr (m < TM)
@@ -246,10 +289,6 @@ struct DmaGemm {
                     else
                         fb[cur ^ 1][m - TM] =
                             frag(stage + L::W_ROW * BK, wn * WN + (m - TM) * 32 + lr, ks + 1);
-                }
-                if constexpr (ks < ISSUE_KS && m < PER) {
-                    constexpr int slot = ks * PER + m;
-                    if (more) issue_range<slot * NDMA / SLOTS, (slot + 1) * NDMA / SLOTS>(next, kt_next);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             });
@@ -384,7 +423,7 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
             g.wait_tile(kt);
             stage_barrier();
             g.compute(stage(s), stage(std::integral_constant<int, NEXT>{}), kt + NS - 1,
-                      kt + NS - 1 < g.nk);
+                      kt + NS - 1 < g.nk, kt > 0);
         }
     };
 
@@ -407,6 +446,7 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
     if (kt + 4 < g.nk) step(std::integral_constant<int, 4>{}, kt + 4);
     if (kt + 5 < g.nk) step(std::integral_constant<int, 5>{}, kt + 5);
     if (kt + 6 < g.nk) step(std::integral_constant<int, 6>{}, kt + 6);
+    g.finish();   // the last tile's deferred MFMAs
 
     // Epilogue. The MFMAs were issued as W x A^T, so each 32x32 accumulator
     // holds a tile of C^T: lane l owns C row (l % 32) of the tile, and
