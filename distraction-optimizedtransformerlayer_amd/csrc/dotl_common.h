@@ -91,11 +91,59 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 // ---- device helpers --------------------------------------------------------
 
+// One step of a wavefront's xor butterfly: v + (v of lane l ^ OFF). The
+// partner's value comes by the cheapest exact route on gfx950 instead of a
+// ds_bpermute (an LDS round trip) every step: v_permlane32_swap /
+// v_permlane16_swap across the 32- and 16-lane halves (with v in both
+// operands, the two results are v and the partner's v), ds_swizzle (xor
+// mode, within 32 lanes) for 8 and 4, DPP quad permutations for 2 and 1.
+// Each lane gets exactly the sum __shfl_xor would give (fp addition
+// commutes), so butterflies written either way agree bit for bit.
+template <int OFF>
+__device__ __forceinline__ float xor_add(float v) {
+    static_assert(OFF == 32 || OFF == 16 || OFF == 8 || OFF == 4 || OFF == 2 || OFF == 1,
+                  "a power-of-two lane offset below 64");
+    if constexpr (OFF == 32) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                         false, false);
+        return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    } else if constexpr (OFF == 16) {
+        const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                         false, false);
+        return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    } else if constexpr (OFF == 8 || OFF == 4) {
+        // bitmask mode: and 0x1f, or 0, xor OFF
+        return v + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (OFF << 10)));
+    } else {
+        // quad_perm [2,3,0,1] (xor 2) or [1,0,3,2] (xor 1)
+        constexpr int kQuad = OFF == 2 ? 0x4E : 0xB1;
+        return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kQuad, 0xF, 0xF,
+                                                              false));
+    }
+}
+
+// The full butterfly (offsets 32, 16, ..., 1) over K values at once, their
+// steps interleaved so one value's fetch latency hides under the others'.
+template <int OFF, int K>
+__device__ __forceinline__ void xor_step(float (&v)[K]) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = xor_add<OFF>(v[k]);
+}
+template <int K>
+__device__ __forceinline__ void wave_sum_n(float (&v)[K]) {
+    xor_step<32>(v);
+    xor_step<16>(v);
+    xor_step<8>(v);
+    xor_step<4>(v);
+    xor_step<2>(v);
+    xor_step<1>(v);
+}
+
 // Butterfly sum over the full 64-lane wavefront. Every lane ends with the total.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
+    float a[1] = {v};
+    wave_sum_n<1>(a);
+    return a[0];
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -158,6 +206,42 @@ constexpr float kLoUnscale = 1.0f / 4096.0f;
 
 __device__ __forceinline__ _Float16 split_lo(float x, _Float16 hi) {
     return static_cast<_Float16>((x - static_cast<float>(hi)) * kLoScale);
+}
+
+// Storage type of each normed-output code.
+template <int NORMED> struct normed_type { using type = float; };
+template <> struct normed_type<DOTL_F16> { using type = _Float16; };
+template <> struct normed_type<DOTL_F16X2> { using type = _Float16; };
+template <> struct normed_type<DOTL_BF16> { using type = __bf16; };
+
+// A value the compiler must treat as computed: narrowing it cannot be fused
+// into the multiply-add that produced it. Left free, the backend may turn
+// fp32 fma + fp16 conversion into one v_fma_mixlo_f16 (a single rounding to
+// fp16), which differs in the last fp16 bit from the fp32 result narrowed
+// with RNE -- the arithmetic the reference and every other kernel here use --
+// and whether it does depends on the surrounding code.
+__device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
+
+// Four normalised values to a LayerNorm's normed output (split planes: hi,
+// then lo in the second plane, `plane` elements further on).
+template <int NORMED>
+__device__ __forceinline__ void store_normed4(void* __restrict__ normed, int64_t plane,
+                                             int64_t off, float4 o) {
+    using TO = typename normed_type<NORMED>::type;
+    TO* out = static_cast<TO*>(normed);
+    if constexpr (NORMED != DOTL_F32) {
+        opaque(o.x); opaque(o.y); opaque(o.z); opaque(o.w);
+    }
+    if constexpr (NORMED == DOTL_F16X2) {
+        half4 h, l;
+        h[0] = to_half(o.x); h[1] = to_half(o.y); h[2] = to_half(o.z); h[3] = to_half(o.w);
+        l[0] = split_lo(o.x, h[0]); l[1] = split_lo(o.y, h[1]);
+        l[2] = split_lo(o.z, h[2]); l[3] = split_lo(o.w, h[3]);
+        *reinterpret_cast<half4*>(out + off) = h;
+        *reinterpret_cast<half4*>(out + plane + off) = l;
+    } else {
+        store4f(out + off, o);
+    }
 }
 
 }  // namespace dotl

@@ -41,6 +41,11 @@ bool launch_gemm_dma(const _Float16* A, const _Float16* Alo, const _Float16* W,
                      const _Float16* Wlo, const float* bias, const float* R, void* C, int64_t M,
                      int64_t N, int64_t K, int mode, int act, int out_dtype, int tile,
                      hipStream_t stream);
+bool launch_gemm_dma_ln(const _Float16* A, const _Float16* W, const float* bias, const float* R,
+                        float* C, int64_t M, int64_t N, int64_t K, const float* ln_w,
+                        const float* ln_b, float eps, void* normed, int normed_dtype,
+                        int64_t plane, const int32_t* out_row, const int64_t* io, int tile,
+                        hipStream_t stream);
 
 namespace {
 
@@ -465,7 +470,7 @@ int linear_impl(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
     DOTL_REQUIRE(math != DOTL_MATH_FP16X3 || w_lo != nullptr,
                  "%s: the fp16x3 math needs the split weight residual", who);
     DOTL_REQUIRE(((M + 63) / 64) * ((N + 63) / 64) <= 0x7fffffff, "%s: too large", who);
-    DOTL_REQUIRE(tile == -1 || (tile >= 0 && tile <= 17) || (tile >= 100 && tile <= 104),
+    DOTL_REQUIRE(tile == -1 || (tile >= 0 && tile <= 18) || (tile >= 100 && tile <= 104),
                  "%s: unknown tile id %d", who, tile);
     if (M == 0 || N == 0) return DOTL_OK;
     DOTL_REQUIRE(x && w_hi && bias && out, "%s: null pointer", who);
@@ -547,4 +552,51 @@ extern "C" int dotl_linear_residual(const void* x, int x_dtype, const void* w_hi
                  "linear_bias: the residual must be 16-byte aligned");
     return linear_impl(x, x_dtype, w_hi, w_lo, bias, residual, out, DOTL_F32, M, N, K, act, math,
                        tile, stream);
+}
+
+extern "C" int dotl_linear_layernorm(const void* x, int x_dtype, const void* w_hi,
+                                     const float* bias, const float* residual, float* out,
+                                     const float* ln_weight, const float* ln_bias, double eps,
+                                     void* normed, int normed_dtype, const int32_t* out_row,
+                                     int64_t normed_rows, const int64_t* io, int64_t M, int64_t N,
+                                     int64_t K, int tile, void* stream) {
+    using namespace dotl;
+    clear_error();
+    const char* who = "linear_layernorm";
+    DOTL_REQUIRE(M >= 0 && N >= 0 && K >= 0 && normed_rows >= 0, "%s: negative extent", who);
+    DOTL_REQUIRE(normed_dtype == DOTL_F32 || normed_dtype == DOTL_F16 ||
+                     normed_dtype == DOTL_F16X2,
+                 "%s: the normed output is float32, float16 or split float16", who);
+    DOTL_REQUIRE(out_row != nullptr || normed_rows == M,
+                 "%s: without out_row the normed output has the product's %lld rows", who,
+                 static_cast<long long>(M));
+    DOTL_REQUIRE(out_row == nullptr || normed_dtype == DOTL_F32,
+                 "%s: scattered rows (out_row) take a float32 normed output", who);
+    DOTL_REQUIRE(tile == -1 || tile == 18, "%s: tile %d (18, 128x256, takes a row LayerNorm)",
+                 who, tile);
+    if (x_dtype != DOTL_F16 || N > 256 || N % 4 != 0 || K % 64 != 0 || K == 0 ||
+        M * K * 2 >= (int64_t{1} << 32) || N * K * 2 >= (int64_t{1} << 32)) {
+        set_error(std::string(who) + ": served for a float16 x, N a multiple of 4 up to 256, "
+                  "K a positive multiple of 64 and operands under 4 GiB; run the GEMM and the "
+                  "LayerNorm separately");
+        return DOTL_DECLINED;
+    }
+    if (M == 0 || N == 0) return DOTL_OK;
+    DOTL_REQUIRE(x && w_hi && bias && ln_weight && ln_bias && (normed || io), "%s: null pointer",
+                 who);
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_hi) |
+                            reinterpret_cast<uintptr_t>(residual) |
+                            reinterpret_cast<uintptr_t>(out) |
+                            reinterpret_cast<uintptr_t>(ln_weight) |
+                            reinterpret_cast<uintptr_t>(ln_bias) |
+                            reinterpret_cast<uintptr_t>(normed);
+    DOTL_REQUIRE(align % 16 == 0, "%s: every tensor must be 16-byte aligned", who);
+    const int t = 18;   // 128x256: a row per wave instruction
+    const bool ok = launch_gemm_dma_ln(static_cast<const _Float16*>(x),
+                                       static_cast<const _Float16*>(w_hi), bias, residual, out, M,
+                                       N, K, ln_weight, ln_bias, static_cast<float>(eps), normed,
+                                       normed_dtype, normed_rows * N, out_row, io, t,
+                                       as_stream(stream));
+    DOTL_REQUIRE(ok, "%s: tile %d is not built with the LayerNorm epilogue", who, t);
+    return check_launch(who);
 }

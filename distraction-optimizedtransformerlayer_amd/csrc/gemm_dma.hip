@@ -73,4 +73,26 @@ bool launch_gemm_dma(const _Float16* A, const _Float16* Alo, const _Float16* W,
     return false;
 }
 
+bool launch_gemm_dma_ln(const _Float16* A, const _Float16* W, const float* bias, const float* R,
+                        float* C, int64_t M, int64_t N, int64_t K, const float* ln_w,
+                        const float* ln_b, float eps, void* normed, int normed_dtype,
+                        int64_t plane, const int32_t* out_row, const int64_t* io, int tile,
+                        hipStream_t stream) {
+    const DmaArgs a{A, nullptr, W, nullptr, bias, R, C, M, N, K, stream};
+    const gemm_dma::LnEpi ln{ln_w, ln_b, eps, normed, plane, out_row, io};
+    const bool wc = C != nullptr;
+    switch (normed_dtype) {
+        case DOTL_F32:
+            return wc ? gemm_dma::dispatch_tile_ln<DOTL_F32 + 4>(a, ln, tile)
+                      : gemm_dma::dispatch_tile_ln<DOTL_F32>(a, ln, tile);
+        case DOTL_F16:
+            return wc ? gemm_dma::dispatch_tile_ln<DOTL_F16 + 4>(a, ln, tile)
+                      : gemm_dma::dispatch_tile_ln<DOTL_F16>(a, ln, tile);
+        case DOTL_F16X2:
+            return wc ? gemm_dma::dispatch_tile_ln<DOTL_F16X2 + 4>(a, ln, tile)
+                      : gemm_dma::dispatch_tile_ln<DOTL_F16X2>(a, ln, tile);
+    }
+    return false;
+}
+
 }  // namespace dotl

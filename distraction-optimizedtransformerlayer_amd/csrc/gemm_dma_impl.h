@@ -331,12 +331,14 @@ struct DmaGemm {
     }
 };
 
-template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT, int NWV = 4>
+// LN >= 0: the row LayerNorm epilogue (LnEpi; LN & 3 the normed dtype code,
+// LN & 4 set when C is stored as well).
+template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT, int NWV = 4, int LN = -1>
 __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
     const _Float16* __restrict__ A, const _Float16* __restrict__ Alo,
     const _Float16* __restrict__ W, const _Float16* __restrict__ Wlo,
     const float* __restrict__ bias, const float* __restrict__ R, void* __restrict__ C, int64_t M,
-    int64_t N, int64_t K) {
+    int64_t N, int64_t K, LnEpi ln) {
     using G = DmaGemm<BM, BN, BK, NS, MODE, ACT, OUTT, NWV>;
     using L = typename G::L;
     static_assert(NS >= 2 && NS <= 8, "2 to 8 stages");
@@ -473,7 +475,9 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
     // (C4 ffn_in shape on the 8-wave tile, both with the full-tile paths
     // below: 266-271 us direct, 272-274 staged; C5's equal) and worse on
     // the 4-wave ones, whose waves have no partner to overlap the transpose.
-    constexpr bool STAGED = !(ACT == DOTL_ACT_GELU && OUTT != DOTL_F32);
+    constexpr bool STAGED = LN >= 0 || !(ACT == DOTL_ACT_GELU && OUTT != DOTL_F32);
+    static_assert(LN < 0 || (ACT == DOTL_ACT_NONE && OUTT == DOTL_F32 && BN == 256),
+                  "the LayerNorm epilogue: fp32 rows a wave instruction wide");
     if constexpr (!STAGED) {
         // A tile wholly inside C stores without per-row or per-column tests
         // (the same reason as the staged rounds below).
@@ -536,14 +540,32 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
         if constexpr (NS > 7) if (b == 7) p = st7;
         return reinterpret_cast<float*>(p);
     };
+    // The LayerNorm epilogue: a wave instruction covers one row (64 lanes x
+    // 4 columns), so each lane's columns are the same in every row; their
+    // weights are loaded once.
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 lnw = z4, lnb = z4;
+    void* normed = nullptr;
+    if constexpr (LN >= 0) {
+        normed = ln.io != nullptr ? reinterpret_cast<void*>(ln.io[1]) : ln.normed;
+        const int64_t lcol = g.n0 + (threadIdx.x & 63) * 4;
+        if (lcol < N) {
+            lnw = *reinterpret_cast<const float4*>(ln.w + lcol);
+            lnb = *reinterpret_cast<const float4*>(ln.b + lcol);
+        }
+    }
     stage_barrier();   // every wave is done reading the stages
     // A tile wholly inside C (every tile but the right and bottom edges)
     // takes a copy of the rounds with no per-row or per-column tests: its
     // residual loads and stores are then single 16-byte accesses in a
     // straight line, so the compiler can count them and wait only for what
     // each chunk needs instead of draining every store before the next.
-    auto rounds = [&](auto fullc) {
-        constexpr bool FULL = decltype(fullc)::value;
+    auto rounds = [&](auto kindc) {
+        // 2: the tile lies wholly inside C; 1: an edge tile of a C whose rows
+        // are whole 16-byte chunks (N % 4 == 0); 0: any other edge tile
+        constexpr int KIND = decltype(kindc)::value;
+        constexpr bool FULL = KIND == 2;
+        constexpr bool VEC = KIND >= 1;
         static_for<0, ROUNDS>([&](auto qq) {
             constexpr int q = decltype(qq)::value;
             constexpr int r_lo = q * RR;
@@ -555,6 +577,18 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
             // under the LDS writes and the barrier instead of stalling the
             // store loop once per batch.
             float4 res[OUTT == DOTL_F32 ? PER_T : 1];
+            // and, for a LayerNorm epilogue that scatters its rows, their
+            // output rows (one per wave instruction: lanes share the row)
+            int32_t orow[LN >= 0 ? PER_T : 1];
+            if constexpr (LN >= 0) {
+                if (ln.out_row != nullptr) {
+#pragma unroll
+                    for (int u = 0; u < PER_T; ++u) {
+                        const int64_t row = g.m0 + r_lo + (threadIdx.x + u * THREADS) / CPR;
+                        orow[u] = ln.out_row[row < M ? row : M - 1];
+                    }
+                }
+            }
             if constexpr (OUTT == DOTL_F32) {
                 if (R != nullptr) {
 #pragma unroll
@@ -562,11 +596,17 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
                         const int c = threadIdx.x + u * THREADS;
                         const int64_t row = g.m0 + r_lo + c / CPR;
                         const int64_t col = g.n0 + (c % CPR) * 4;
-                        const float* rrow = R + row * N + col;
-                        if constexpr (FULL) {
-                            res[u] = *reinterpret_cast<const float4*>(rrow);
+                        if constexpr (VEC) {
+                            // unconditional: an edge tile's rows past M and
+                            // chunks past N read the last row / chunk (those
+                            // outputs are never stored), so the loads go out
+                            // back to back instead of each behind a branch
+                            const int64_t rr = FULL ? row : (row < M ? row : M - 1);
+                            const int64_t cc4 = FULL ? col : (col < N - 4 ? col : N - 4);
+                            res[u] = *reinterpret_cast<const float4*>(R + rr * N + cc4);
                             continue;
                         }
+                        const float* rrow = R + row * N + col;
                         res[u] = make_float4(0.f, 0.f, 0.f, 0.f);
                         if (row < M) {
                             if (vec_ok && col + 4 <= N) {
@@ -611,18 +651,18 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
                 }
             }
             stage_barrier();
-            // read + store: row-contiguous chunks of rows [r_lo, r_hi)
-#pragma unroll
-            for (int u = 0; u < PER_T; ++u) {
+            // read + store: row-contiguous chunks of rows [r_lo, r_hi). Chunk
+            // u of this thread: its row, its column, and act(acc + bias)
+            // (+ residual) from the stage buffer.
+            auto value = [&](int u, int64_t& row, int64_t& col) -> float4 {
                 const int c = threadIdx.x + u * THREADS;
                 const int rl = c / CPR;                 // row within the round
                 const int cc = c % CPR;                 // logical chunk
                 const int b = rl / RPB;
                 const int rb = rl % RPB;
-                const int64_t row = g.m0 + r_lo + rl;
+                row = g.m0 + r_lo + rl;
                 const int cl = cc * 4;                  // tile-local column
-                const int64_t col = g.n0 + cl;
-                if (!FULL && row >= M) continue;
+                col = g.n0 + cl;
                 const float4 a4 =
                     *reinterpret_cast<const float4*>(buf(b) + rb * BN + ((cc ^ (rb & 15)) * 4));
                 float v[4] = {a4.x, a4.y, a4.z, a4.w};
@@ -640,30 +680,115 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
                         v[2] = res[u].z + v[2]; v[3] = res[u].w + v[3];
                     }
                 }
-                TO* crow = static_cast<TO*>(C) + row * N;
-                if (FULL || (vec_ok && col + 4 <= N)) {
-                    store4f(crow + col, make_float4(v[0], v[1], v[2], v[3]));
-                } else {
+                return make_float4(v[0], v[1], v[2], v[3]);
+            };
+            if constexpr (LN >= 0) {
+                // Each row's LayerNorm, in the LayerNorm kernels' exact
+                // arithmetic for a row of <= 256 columns held one float4 a
+                // lane (zeros past N): the same sums in the same order, so
+                // the normed values are theirs bit for bit. A wave
+                // instruction covers one row; the thread's rows go through
+                // each step LG at a time, their butterflies interleaved and on
+                // permlane / swizzle / DPP exchanges (one row at a time on
+                // ds_bpermute, every step waited out an LDS round trip; all of
+                // a round's rows at once spilled). Rows past M are reduced too
+                // (wave-uniform) and not stored.
+                static_assert(CPR == 64, "one row a wave instruction");
+                constexpr int LG = PER_T < 4 ? PER_T : 4;
+                static_assert(PER_T % LG == 0, "row groups");
+                const float inv_d = 1.0f / static_cast<float>(N);
+                static_for<0, PER_T / LG>([&](auto gg) {
+                    constexpr int U0 = decltype(gg)::value * LG;
+                    float4 xv[LG];
+                    float mean_est[LG], sd[LG], sd2[LG];
+                    int64_t rows_[LG];
+                    int64_t col = 0;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (col + e < N) crow[col + e] = from_f32<TO>(v[e]);
+                    for (int k = 0; k < LG; ++k) {
+                        const float4 v4 = value(U0 + k, rows_[k], col);
+                        xv[k] = col < N ? v4 : z4;   // N % 4 == 0: whole chunks
+                        mean_est[k] = 0.f;
+                        mean_est[k] += (xv[k].x + xv[k].y) + (xv[k].z + xv[k].w);
+                    }
+                    const bool in = col < N;         // this lane's column, every row
+                    wave_sum_n(mean_est);
+#pragma unroll
+                    for (int k = 0; k < LG; ++k) {
+                        mean_est[k] *= inv_d;
+                        sd[k] = 0.f;
+                        sd2[k] = 0.f;
+                        if (in) {
+                            const float d0 = xv[k].x - mean_est[k], d1 = xv[k].y - mean_est[k];
+                            const float d2 = xv[k].z - mean_est[k], d3 = xv[k].w - mean_est[k];
+                            sd[k] += (d0 + d1) + (d2 + d3);
+                            sd2[k] += ln_sq4(d0, d1, d2, d3);
+                        }
+                    }
+                    {
+                        // sd and sd2 reduced together, as the LayerNorm kernels do
+                        float both[2 * LG];
+#pragma unroll
+                        for (int k = 0; k < LG; ++k) { both[2 * k] = sd[k]; both[2 * k + 1] = sd2[k]; }
+                        wave_sum_n(both);
+#pragma unroll
+                        for (int k = 0; k < LG; ++k) { sd[k] = both[2 * k]; sd2[k] = both[2 * k + 1]; }
+                    }
+#pragma unroll
+                    for (int k = 0; k < LG; ++k) {
+                        const int64_t row = rows_[k];
+                        if (!FULL && row >= M) continue;   // wave-uniform
+                        const float delta = sd[k] * inv_d;
+                        const float var = ln_var(sd2[k], delta, inv_d);
+                        const float rstd = 1.0f / sqrtf(var + ln.eps);
+                        if (in) {
+                            if constexpr ((LN & 4) != 0)
+                                store4f(static_cast<float*>(C) + row * N + col, xv[k]);
+                            float4 o;
+                            o.x = ln_out(xv[k].x, mean_est[k], delta, rstd, lnw.x, lnb.x);
+                            o.y = ln_out(xv[k].y, mean_est[k], delta, rstd, lnw.y, lnb.y);
+                            o.z = ln_out(xv[k].z, mean_est[k], delta, rstd, lnw.z, lnb.z);
+                            o.w = ln_out(xv[k].w, mean_est[k], delta, rstd, lnw.w, lnb.w);
+                            const int64_t nrow = ln.out_row != nullptr ? orow[U0 + k] : row;
+                            store_normed4<(LN & 3)>(normed, ln.plane, nrow * N + col, o);
+                        }
+                    }
+                });
+            } else {
+#pragma unroll
+                for (int u = 0; u < PER_T; ++u) {
+                    int64_t row, col;
+                    // the row test first: a row past M reads nothing
+                    const int c = threadIdx.x + u * THREADS;
+                    if (!FULL && g.m0 + r_lo + c / CPR >= M) continue;
+                    const float4 v4 = value(u, row, col);
+                    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+                    TO* crow = static_cast<TO*>(C) + row * N;
+                    if (FULL || (VEC && col + 4 <= N)) {
+                        store4f(crow + col, v4);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (col + e < N) crow[col + e] = from_f32<TO>(v[e]);
+                    }
                 }
             }
         });
     };
     if (vec_ok && g.m0 + BM <= M && g.n0 + BN <= N)
-        rounds(std::integral_constant<bool, true>{});
+        rounds(std::integral_constant<int, 2>{});
+    else if (vec_ok)
+        rounds(std::integral_constant<int, 1>{});
     else
-        rounds(std::integral_constant<bool, false>{});
+        rounds(std::integral_constant<int, 0>{});
     }
 }
 
-template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT, int NWV = 4>
-void launch_dma(const DmaArgs& a) {
+template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT, int NWV = 4, int LN = -1>
+void launch_dma(const DmaArgs& a, const LnEpi& ln = LnEpi{}) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, MODE, ACT, OUTT, NWV>),
+    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, MODE, ACT, OUTT, NWV, LN>),
                        dim3(static_cast<unsigned>(tiles)), dim3(NWV * 64), 0, a.stream, a.A,
-                       a.Alo, a.W, a.Wlo, a.bias, a.R, a.C, a.M, a.N, a.K);
+                       a.Alo, a.W, a.Wlo, a.bias, a.R, a.C, a.M, a.N, a.K, ln);
 }
 
 // Tile ids (dotl_linear's `tile`): 0 128x128, 1 256x128, 2 64x64, 3 256x256,
@@ -747,6 +872,20 @@ bool dispatch_tile(const DmaArgs& a, int tile) {
         case 17:  // 256x128, 128-byte K rows, 3 stages of 48 KiB
             if constexpr (PASSES == 1) { launch_dma<256, 128, 64, 3, MODE, ACT, OUTT, 8>(a); return true; }
             return false;
+        case 18:  // 128x256, 128-byte K rows, 3 stages of 48 KiB
+            if constexpr (PASSES == 1) { launch_dma<128, 256, 64, 3, MODE, ACT, OUTT, 8>(a); return true; }
+            return false;
+    }
+    return false;
+}
+
+template <int LN>
+bool dispatch_tile_ln(const DmaArgs& a, const LnEpi& ln, int tile) {
+    // 128x256 only: the 256x256 tile's 128 accumulator registers leave no
+    // room for the row reductions (it spilled ~300 registers)
+    if (tile == 18) {
+        launch_dma<128, 256, 64, 3, 0, DOTL_ACT_NONE, DOTL_F32, 8, LN>(a, ln);
+        return true;
     }
     return false;
 }
@@ -765,5 +904,19 @@ bool dispatch_tile(const DmaArgs& a, int tile) {
     template bool dispatch_tile<M, DOTL_ACT_GELU, DOTL_F32>(const DmaArgs&, int);               \
     template bool dispatch_tile<M, DOTL_ACT_GELU, (M == 4 ? DOTL_BF16 : DOTL_F16)>(             \
         const DmaArgs&, int);                                                                   \
+    }                                                                                           \
+    }
+
+// The LayerNorm-epilogue instances (one pass): normed fp32, fp16 or split
+// planes, with and without C stored.
+#define DOTL_GEMM_DMA_INSTANTIATE_LN()                                                          \
+    namespace dotl {                                                                            \
+    namespace gemm_dma {                                                                        \
+    template bool dispatch_tile_ln<DOTL_F32>(const DmaArgs&, const LnEpi&, int);                \
+    template bool dispatch_tile_ln<DOTL_F16>(const DmaArgs&, const LnEpi&, int);                \
+    template bool dispatch_tile_ln<DOTL_F16X2>(const DmaArgs&, const LnEpi&, int);              \
+    template bool dispatch_tile_ln<DOTL_F32 + 4>(const DmaArgs&, const LnEpi&, int);            \
+    template bool dispatch_tile_ln<DOTL_F16 + 4>(const DmaArgs&, const LnEpi&, int);            \
+    template bool dispatch_tile_ln<DOTL_F16X2 + 4>(const DmaArgs&, const LnEpi&, int);          \
     }                                                                                           \
     }

@@ -35,12 +35,6 @@ namespace {
 
 constexpr int kRowsPerBlock = 4;
 
-// Storage type of each normed-output code.
-template <int NORMED> struct normed_type { using type = float; };
-template <> struct normed_type<DOTL_F16> { using type = _Float16; };
-template <> struct normed_type<DOTL_F16X2> { using type = _Float16; };
-template <> struct normed_type<DOTL_BF16> { using type = __bf16; };
-
 // Graph I/O slot (optional): io[0] replaces the x pointer when bit 0 of
 // io_mode is set, io[1] the normed pointer when bit 1 is. A captured graph
 // bakes in the slot's address, not the tensors', so each replay reads the
@@ -62,36 +56,6 @@ __device__ __forceinline__ float4 load_sum4(const TI* __restrict__ x, const TI* 
         a.z = round_via<TI>(a.z + s.z); a.w = round_via<TI>(a.w + s.w);
     }
     return a;
-}
-
-// A value the compiler must treat as computed: narrowing it cannot be fused
-// into the multiply-add that produced it. Left free, the backend may turn
-// fp32 fma + fp16 conversion into one v_fma_mixlo_f16 (a single rounding to
-// fp16), which differs in the last fp16 bit from the fp32 result narrowed
-// with RNE -- the arithmetic the reference and every other kernel here use --
-// and whether it does depends on the surrounding code.
-__device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
-
-// Four normalised values to the normed output (split planes: hi, then lo
-// in the second [rows, D] plane).
-template <int NORMED>
-__device__ __forceinline__ void store_normed4(void* __restrict__ normed, int64_t plane,
-                                             int64_t off, float4 o) {
-    using TO = typename normed_type<NORMED>::type;
-    TO* out = static_cast<TO*>(normed);
-    if constexpr (NORMED != DOTL_F32) {
-        opaque(o.x); opaque(o.y); opaque(o.z); opaque(o.w);
-    }
-    if constexpr (NORMED == DOTL_F16X2) {
-        half4 h, l;
-        h[0] = to_half(o.x); h[1] = to_half(o.y); h[2] = to_half(o.z); h[3] = to_half(o.w);
-        l[0] = split_lo(o.x, h[0]); l[1] = split_lo(o.y, h[1]);
-        l[2] = split_lo(o.z, h[2]); l[3] = split_lo(o.w, h[3]);
-        *reinterpret_cast<half4*>(out + off) = h;
-        *reinterpret_cast<half4*>(out + plane + off) = l;
-    } else {
-        store4f(out + off, o);
-    }
 }
 
 template <int NORMED>
@@ -180,10 +144,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
             for (int c = 0; c < CH; ++c) s_ += (v[r][c].x + v[r][c].y) + (v[r][c].z + v[r][c].w);
             mean_est[r] = s_;
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1)
-#pragma unroll
-            for (int r = 0; r < RPW; ++r) mean_est[r] += __shfl_xor(mean_est[r], off, kWave);
+        wave_sum_n(mean_est);
         float sd[RPW], sd2[RPW];
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
@@ -201,13 +162,14 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
                 }
             }
         }
+        {
+            float both[2 * RPW];
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1)
+            for (int r = 0; r < RPW; ++r) { both[2 * r] = sd[r]; both[2 * r + 1] = sd2[r]; }
+            wave_sum_n(both);
 #pragma unroll
-            for (int r = 0; r < RPW; ++r) {
-                sd[r] += __shfl_xor(sd[r], off, kWave);
-                sd2[r] += __shfl_xor(sd2[r], off, kWave);
-            }
+            for (int r = 0; r < RPW; ++r) { sd[r] = both[2 * r]; sd2[r] = both[2 * r + 1]; }
+        }
 
         // x - mean as (x - m) - delta: x - m is exact (both near the mean),
         // whereas forming m + delta first would round the mean to ulp(mean).
@@ -301,10 +263,11 @@ __global__ __launch_bounds__(256) void layernorm_scalar_kernel(
                 sd2 = fmaf(d, d, sd2);
             }
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            sd += __shfl_xor(sd, off, kWave);
-            sd2 += __shfl_xor(sd2, off, kWave);
+        {
+            float both[2] = {sd, sd2};
+            wave_sum_n(both);
+            sd = both[0];
+            sd2 = both[1];
         }
         const float delta = sd * inv_d;
         const float var = ln_var(sd2, delta, inv_d);
@@ -475,4 +438,43 @@ extern "C" int dotl_bind_io(int64_t* slot, const void* in, void* out, void* stre
                        static_cast<int64_t>(reinterpret_cast<uintptr_t>(in)),
                        static_cast<int64_t>(reinterpret_cast<uintptr_t>(out)));
     return check_launch("bind_io");
+}
+
+// Zero rows of a padded output: one wave per row, rows with row_map[r] >= 0
+// (written by the producer) left alone.
+namespace dotl {
+namespace {
+__global__ __launch_bounds__(256) void zero_rows_kernel(float* __restrict__ out,
+                                                        const int32_t* __restrict__ row_map,
+                                                        int64_t rows, int64_t width,
+                                                        const int64_t* __restrict__ io) {
+    if (io != nullptr) out = reinterpret_cast<float*>(io[1]);
+    const int lane = threadIdx.x & 63;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kRowsPerBlock;
+    for (int64_t r = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+         r < rows; r += stride) {
+        if (row_map[r] >= 0) continue;   // wave-uniform
+        float* row = out + r * width;
+        if ((width & 3) == 0) {
+            for (int64_t c = 4 * lane; c < width; c += 256)
+                *reinterpret_cast<float4*>(row + c) = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+            for (int64_t c = lane; c < width; c += 64) row[c] = 0.f;
+        }
+    }
+}
+}  // namespace
+}  // namespace dotl
+
+extern "C" int dotl_zero_rows(float* out, const int32_t* row_map, int64_t rows, int64_t width,
+                              const int64_t* io, void* stream) {
+    using namespace dotl;
+    clear_error();
+    DOTL_REQUIRE(rows >= 0 && width >= 0, "zero_rows: negative extent");
+    if (rows == 0 || width == 0) return DOTL_OK;
+    DOTL_REQUIRE((out || io) && row_map, "zero_rows: null pointer");
+    DOTL_REQUIRE(reinterpret_cast<uintptr_t>(out) % 16 == 0, "zero_rows: out must be 16-byte aligned");
+    hipLaunchKernelGGL(zero_rows_kernel, dim3(grid_for(rows)), dim3(256), 0, as_stream(stream), out,
+                       row_map, rows, width, io);
+    return check_launch("zero_rows");
 }

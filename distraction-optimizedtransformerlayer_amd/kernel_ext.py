@@ -60,7 +60,7 @@ EXPORTED_SYMBOLS = (
     "dotl_attention_set_pipeline", "dotl_linear_residual", "dotl_bind_io",
     "dotl_attention_split_plan", "dotl_wmma_set_split_kv", "dotl_wmma_split_kv_enabled",
     "dotl_wmma_set_split_count", "dotl_attention_forward_noalloc",
-    "dotl_attention_noalloc_scratch_bytes",
+    "dotl_attention_noalloc_scratch_bytes", "dotl_linear_layernorm", "dotl_zero_rows",
 )
 
 _kernels = None
@@ -118,6 +118,11 @@ def _declare(lib) -> None:
     lib.dotl_linear_residual.restype = i32
     lib.dotl_linear_residual.argtypes = [vp, i32, vp, vp, vp, vp, vp, i64, i64, i64, i32, i32,
                                          i32, vp]
+    lib.dotl_linear_layernorm.restype = i32
+    lib.dotl_linear_layernorm.argtypes = [vp, i32, vp, vp, vp, vp, vp, vp, c.c_double, vp, i32,
+                                          vp, i64, vp, i64, i64, i64, i32, vp]
+    lib.dotl_zero_rows.restype = i32
+    lib.dotl_zero_rows.argtypes = [vp, vp, i64, i64, vp, vp]
     lib.dotl_attention_forward.restype = i32
     lib.dotl_attention_forward.argtypes = [vp, vp, vp, i32, c.POINTER(i64), vp, c.POINTER(i64),
                                            vp, i32, i32, i32, i32, i32, i32, i32, c.c_double,
@@ -529,6 +534,98 @@ class Kernels:
         if rc == DOTL_DECLINED:
             return None
         return out
+
+    def linear_layernorm(self, x, weight, bias, residual, ln_weight, ln_bias, eps=1e-5,
+                         normed="float", store_out=True, out_row=None, normed_rows=None,
+                         tile=-1, io=None):
+        """(h, LayerNorm(h)) with h = residual + x @ weight^T + bias, in one
+        GEMM whose epilogue normalises each row (rows of up to 256 columns).
+
+        Not in the reference's surface: linear_bias(residual=...) followed by
+        fused_layernorm, bit for bit. `x` fp16 [..., K]; `normed` "float",
+        "half" or "split" (fp16 hi/lo planes [2, rows, N]); `store_out` False
+        skips h (None is returned for it). With `out_row` (int32 [M], device)
+        row r of the normed output goes to row out_row[r] of a [normed_rows,
+        N] fp32 tensor whose other rows are left as allocated (zero them with
+        zero_rows). `io` = (slot, 2) binds the normed pointer to a graph I/O
+        slot as the LayerNorm methods do. Returns None where the kernel
+        declines (the caller runs the two ops)."""
+        import torch
+
+        who = "linear_layernorm"
+        self._require_cuda(who, x, weight, bias, residual, ln_weight, ln_bias, out_row)
+        if weight.dim() != 2 or x.shape[-1] != weight.shape[1]:
+            raise RuntimeError(f"{who}: x [..., K] and weight [N, K] required")
+        if x.dtype != torch.float16 or weight.dtype != torch.float32 or bias.dtype != torch.float32:
+            return None
+        N, K = weight.shape
+        if (ln_weight.numel() != N or ln_bias.numel() != N or ln_weight.dtype != torch.float32
+                or ln_bias.dtype != torch.float32):
+            raise RuntimeError(f"{who}: LayerNorm weight/bias must be float32 with {N} elements")
+        xc = x.contiguous()
+        M = xc.numel() // K
+        shape = (*xc.shape[:-1], N)
+        hi, _ = self.weight_half(weight, False)
+        rc_ = None
+        if residual is not None:
+            if residual.dtype != torch.float32 or tuple(residual.shape) != tuple(shape):
+                raise RuntimeError(f"{who}: residual must be float32 of shape {tuple(shape)}")
+            rc_ = residual.contiguous()
+        out = torch.empty(shape, dtype=torch.float32, device=xc.device) if store_out else None
+        if out_row is not None:
+            if out_row.dtype != torch.int32 or out_row.numel() != M or normed != "float":
+                raise RuntimeError(f"{who}: out_row must be int32 [{M}] with a float normed output")
+            if normed_rows is None:
+                raise RuntimeError(f"{who}: out_row needs normed_rows")
+            nshape = (int(normed_rows), N)
+        else:
+            normed_rows = M
+            nshape = shape
+        if normed == "split":
+            nout = torch.empty((2, *nshape), dtype=torch.float16, device=xc.device)
+            ncode = DOTL_F16X2
+        elif normed == "half":
+            nout = torch.empty(nshape, dtype=torch.float16, device=xc.device)
+            ncode = DOTL_F16
+        elif normed == "float":
+            nout = torch.empty(nshape, dtype=torch.float32, device=xc.device)
+            ncode = DOTL_F32
+        else:
+            raise RuntimeError(f"{who}: normed must be 'float', 'half' or 'split'")
+        slot_ptr = None
+        if io is not None:
+            slot, mode = io
+            if mode != 2 or slot.dtype != torch.int64 or slot.numel() < 2 or not slot.is_cuda:
+                raise RuntimeError(f"{who}: io must be (a CUDA int64 slot of 2, 2)")
+            slot_ptr = slot.data_ptr()
+        orc = out_row.contiguous() if out_row is not None else None
+        rc = self._check(self._lib.dotl_linear_layernorm(
+            xc.data_ptr(), DOTL_F16, hi.data_ptr(), bias.contiguous().data_ptr(),
+            rc_.data_ptr() if rc_ is not None else None,
+            out.data_ptr() if out is not None else None, ln_weight.contiguous().data_ptr(),
+            ln_bias.contiguous().data_ptr(), float(eps), nout.data_ptr(), ncode,
+            orc.data_ptr() if orc is not None else None, int(normed_rows), slot_ptr, M, N, K,
+            int(tile), self._stream(x.device)))
+        if rc == DOTL_DECLINED:
+            return None
+        return out, nout
+
+    def zero_rows(self, out, row_map, io=None):
+        """Zero row r of the fp32 [rows, width] `out` wherever row_map[r] < 0
+        (int32 [rows]): the padded rows of a scattered output. `io` = (slot,
+        2): out is the slot's bound output. Not in the reference's surface."""
+        import torch
+
+        self._require_cuda("zero_rows", out, row_map)
+        if out.dtype != torch.float32 or row_map.dtype != torch.int32:
+            raise RuntimeError("zero_rows: out float32 and row_map int32 required")
+        width = out.shape[-1]
+        rows = out.numel() // width if width else 0
+        if row_map.numel() != rows:
+            raise RuntimeError(f"zero_rows: row_map must have {rows} entries")
+        slot_ptr = io[0].data_ptr() if io is not None else None
+        self._check(self._lib.dotl_zero_rows(out.data_ptr(), row_map.contiguous().data_ptr(),
+                                             rows, width, slot_ptr, self._stream(out.device)))
 
     def bias_f32(self, bias):
         """An fp32 copy of a 16-bit bias (the epilogue adds in fp32), cached

@@ -6,11 +6,12 @@ through the module (`config.CUDA_GRAPH = "off"`): a `from ... import` binds
 the value, not the setting. The thresholds below were re-derived for MI355X
 (256 CUs, 288 GB HBM3E) rather than carried over from the reference's card.
 
-Five knobs are new in this build:
+Six knobs are new in this build:
   QKV_PRECISION  arithmetic of the fused QKV projection (auto, fp16x2, fp16x3, fp16)
   GELU_FP16      whether linear_gelu stores its output as fp16 for ffn_out
   ROW_PACKING    whether a padded batch runs on its valid rows only
   RESIDUAL_EPILOGUE  whether out_proj and ffn_out add the residual stream
+  LN_EPILOGUE    whether they also apply the following LayerNorm (narrow rows)
 """
 
 # Attention backend. One legal value: the custom kernels, never a prebuilt
@@ -155,6 +156,19 @@ ROW_PACKING = "auto"
 # 35.4, C2 96.0 / 93.6, C3 268.6 / 268.7, C5 574 / 544.
 RESIDUAL_EPILOGUE = "auto"
 _RESIDUAL_EPILOGUE_MIN_D = 0
+
+# The LayerNorm after out_proj and after ffn_out in the same GEMM's epilogue
+# (with the residual epilogue on): "auto" where one workgroup's tile spans a
+# whole row (d_model <= _LN_EPILOGUE_MAX_D, a multiple of 4): the epilogue
+# normalises each row with the LayerNorm kernels' arithmetic (bit-identical
+# outputs) and the LayerNorm launches and their reads of the residual
+# stream go away; "off" keeps the separate LayerNorms.
+LN_EPILOGUE = "auto"
+_LN_EPILOGUE_MAX_D = 256
+# ... and from this many rows: the one tile built with it (128x256, one
+# workgroup a CU) needs a few hundred tiles. Same-box A/B (layer µs, on /
+# off): C5 (85 104 rows) 518 / 530; C1 (128 rows, one tile) 54.6 / 35.4.
+_LN_EPILOGUE_MIN_ROWS = 32768
 
 # Arithmetic of a model with more than one block. Each block's fp16 operand
 # roundings add to the residual stream the next block reads, so the error at

@@ -425,6 +425,58 @@ def _residual_epilogue_wanted(width_in: int) -> bool:
             and width_in % 64 == 0 and width_in >= config._RESIDUAL_EPILOGUE_MIN_D)
 
 
+def _ln_epilogue_wanted(rows: int, width: int) -> bool:
+    """Apply the LayerNorm after out_proj / ffn_out in that GEMM's epilogue
+    (one workgroup's tile spans the whole row)?"""
+    return (config.LN_EPILOGUE != "off" and config.LAYERNORM != "off" and _lb() == "auto"
+            and width % 4 == 0 and width <= config._LN_EPILOGUE_MAX_D
+            and rows >= config._LN_EPILOGUE_MIN_ROWS)
+
+
+def _linear_norm(x: torch.Tensor, lin, residual: torch.Tensor, norm, kind: str,
+                 store_out: bool = True, packing=None, output: bool = False):
+    """(residual + lin(x), norm of that): `kind` is the normed form, "float",
+    "half" (fp16) or "split" (fp16 hi/lo planes).
+
+    One GEMM whose epilogue adds the residual and normalises each row where
+    _ln_epilogue_wanted (bit-identical to the two kernels); else the GEMM
+    with its residual epilogue, then the LayerNorm. With `packing` the normed
+    rows land in the padded [B, S, D] layout with zero padded rows (the
+    model's output norm, always fp32). `output`: the normed tensor is the
+    forward's output (a captured graph's output slot). `store_out` False:
+    the caller does not read the sum (None may come back for it).
+    """
+    width = lin.weight.shape[0]
+    rows = x.numel() // x.shape[-1]
+    if _ln_epilogue_wanted(rows, width) and x.dtype == torch.float16 and lin.bias is not None:
+        kernels = _custom_kernels()
+        if kernels is not None:
+            io = _output_io() if output else None
+            if packing is not None:
+                res = kernels.linear_layernorm(
+                    x, lin.weight, lin.bias, residual, norm.weight, norm.bias, norm.eps,
+                    normed="float", store_out=store_out, out_row=packing.idx,
+                    normed_rows=packing.batch * packing.seq_len, io=io)
+                if res is not None:
+                    h, out = res
+                    kernels.zero_rows(out, packing.inv, io=io)
+                    out = _note_output(out, io)
+                    return h, out.view(packing.batch, packing.seq_len, width)
+            else:
+                res = kernels.linear_layernorm(x, lin.weight, lin.bias, residual, norm.weight,
+                                               norm.bias, norm.eps, normed=kind,
+                                               store_out=store_out, io=io)
+                if res is not None:
+                    h, out = res
+                    return h, _note_output(out, io)
+    h = _linear_bias(x, lin.weight, lin.bias, residual=residual)
+    if packing is not None:
+        return h, _layernorm_unpack(h, norm, packing)
+    if kind == "split":
+        return h, _layernorm_split(h, norm)
+    return h, _layernorm(h, norm, out_half=kind == "half", output=output)
+
+
 def _ffn_block_eligible(x, ffn_in, ffn_out) -> bool:
     """Would _ffn_block run the fused kernel for this block (rather than decline)?"""
     if config.FFN_BLOCK == "off":

@@ -17,9 +17,10 @@ from .kernels import (_add_layernorm, _add_layernorm_output, _add_layernorm_spli
                       _add_layernorm_unpack,
                       _attention_dispatch, _attention_packed, _attention_wants_fp16,
                       _ffn_block, _ffn_block_eligible, _gelu_input_wants_fp16,
-                      _gelu_output_wants_fp16, _layernorm, _layernorm_split, _layernorm_unpack,
-                      _linear_bias, _linear_bias_split, _linear_gelu, _normed_split_wanted,
-                      _normed_wants_fp16, _qkv_math_code, _residual_epilogue_wanted)
+                      _gelu_output_wants_fp16, _layernorm, _layernorm_split,
+                      _linear_bias, _linear_bias_split, _linear_gelu, _linear_norm,
+                      _normed_split_wanted, _normed_wants_fp16, _qkv_math_code,
+                      _residual_epilogue_wanted)
 from .util import _version_or_none
 
 
@@ -99,7 +100,8 @@ class MySelfAttention(nn.Module):
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,
                 causal: bool = False, mask_is_trivial: bool = False,
-                packing=None, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+                packing=None, residual: Optional[torch.Tensor] = None,
+                norm: Optional["MyLayerNorm"] = None, norm_kind: str = "float"):
         """`x` is [B, S, D], or [2, B, S, D] split fp16 planes of it (the form
         a LayerNorm emits for the split QKV projection).
 
@@ -109,10 +111,12 @@ class MySelfAttention(nn.Module):
         rows to zero.
 
         With `residual` (not on the masked padded path) the result is
-        residual + out_proj(...), the add done in out_proj's epilogue.
+        residual + out_proj(...), the add done in out_proj's epilogue; with
+        `norm` as well, the pair (that sum, norm of it in form `norm_kind`),
+        the LayerNorm in the same epilogue where the row is narrow enough.
         """
         if packing is not None:
-            return self._forward_packed(x, causal, packing, residual)
+            return self._forward_packed(x, causal, packing, residual, norm, norm_kind)
         split = x.dim() == 4
         batch, seq_len = (x.shape[1], x.shape[2]) if split else (x.shape[0], x.shape[1])
         qkv_w, qkv_b = self._get_qkv_weight()
@@ -135,6 +139,8 @@ class MySelfAttention(nn.Module):
         context = _attention_dispatch(q, k, v, attn_mask=attn_mask, is_causal=causal,
                                       scale=self.scale)
         if residual is not None and not use_mask:
+            if norm is not None:
+                return _linear_norm(context, self.out_proj, residual, norm, norm_kind)
             return _linear_bias(context, self.out_proj.weight, self.out_proj.bias,
                                 residual=residual)
         output = self.out_proj(context)
@@ -145,7 +151,8 @@ class MySelfAttention(nn.Module):
         return output
 
     def _forward_packed(self, x: torch.Tensor, causal: bool, packing,
-                        residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+                        residual: Optional[torch.Tensor] = None,
+                        norm: Optional["MyLayerNorm"] = None, norm_kind: str = "float"):
         split = x.dim() == 3
         rows = packing.t_valid
         qkv_w, qkv_b = self._get_qkv_weight()
@@ -159,6 +166,8 @@ class MySelfAttention(nn.Module):
         q, k, v = qkv.view(rows, 3, self.num_heads, self.head_dim).unbind(1)
         context = _attention_packed(q, k, v, packing, causal, self.scale)
         if residual is not None:
+            if norm is not None:
+                return _linear_norm(context, self.out_proj, residual, norm, norm_kind)
             return _linear_bias(context, self.out_proj.weight, self.out_proj.bias,
                                 residual=residual)
         return self.out_proj(context)
@@ -242,21 +251,26 @@ class MyTransformerBlock(nn.Module):
     def _forward_residual_fused(self, x, normed, next_norm, next_norm_is_output, packing=None):
         """The block with h1 = x + out_proj(...) and h2 = h1 + ffn_out(...)
         formed in the GEMM epilogues (the same fp32 sums the add+LayerNorm
-        kernels would form), followed by plain LayerNorms of h1 and h2.
-        Outputs are bit-identical to the add+LayerNorm chain."""
+        kernels would form), each followed by its LayerNorm -- in the same
+        epilogue where the rows are narrow enough (_linear_norm), else as a
+        plain LayerNorm of h1 / h2. Outputs are bit-identical to the
+        add+LayerNorm chain."""
         rows = x.numel() // x.shape[-1]
         width = x.shape[-1]
-        h1 = self.attention(normed, None, self.causal, True, packing=packing, residual=x)
-        normed2 = _layernorm(h1, self.norm2, out_half=_gelu_input_wants_fp16(rows, width))
+        kind2 = "half" if _gelu_input_wants_fp16(rows, width) else "float"
+        h1, normed2 = self.attention(normed, None, self.causal, True, packing=packing, residual=x,
+                                     norm=self.norm2, norm_kind=kind2)
         hidden = _linear_gelu(normed2, self.ffn_in, out_half=_gelu_output_wants_fp16(rows))
-        h2 = _linear_bias(hidden, self.ffn_out.weight, self.ffn_out.bias, residual=h1)
         if next_norm_is_output:
-            if packing is not None:
-                return None, _layernorm_unpack(h2, next_norm, packing)
-            return h2, _final_norm(h2, next_norm)
+            # the model's output: never narrowed; the sum is not read after it
+            h2, out = _linear_norm(hidden, self.ffn_out, h1, next_norm, "float", store_out=False,
+                                   packing=packing, output=True)
+            return (None if packing is not None else h2), out
         if _normed_split_wanted():
-            return h2, _layernorm_split(h2, next_norm)
-        return h2, _layernorm(h2, next_norm, out_half=_normed_wants_fp16(rows, width))
+            kind = "split"
+        else:
+            kind = "half" if _normed_wants_fp16(rows, width) else "float"
+        return _linear_norm(hidden, self.ffn_out, h1, next_norm, kind)
 
     def _forward_packed(self, x, normed, next_norm, next_norm_is_output, packing):
         if self._residual_fused(x):

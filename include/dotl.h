@@ -209,6 +209,47 @@ int dotl_linear_residual(const void* x, int x_dtype, const void* w_hi, const voi
                          int64_t N, int64_t K, int act, int math, int tile, void* stream);
 
 /*
+ * h = residual + x @ W^T + bias (fp32 [M, N]) and normed = LayerNorm(h) *
+ * ln_weight + ln_bias in one kernel: linear_bias followed by the reference's
+ * fused_add_layernorm (csrc/linear_gelu.cuh:598-719, then
+ * csrc/add_layernorm.cuh:491-692: x_new = x + sub, normed with the biased
+ * variance and fp32 statistics), for rows of up to 256 columns, which one
+ * workgroup's tile spans. The LayerNorm is the LayerNorm kernels' own
+ * arithmetic, so both outputs equal dotl_linear_residual + dotl_layernorm
+ * bit for bit. No counterpart entry in the reference.
+ *   x            fp16 [M, K], K a positive multiple of 64 (one fp16 pass)
+ *   w_hi         fp16 [N, K] (dotl_weight_split); bias fp32 [N]
+ *   residual     optional (NULL) fp32 [M, N]
+ *   out          optional (NULL: h is not stored) fp32 [M, N]
+ *   normed       [normed_rows, N] in normed_dtype: DOTL_F32, DOTL_F16 (RNE)
+ *                or DOTL_F16X2 (split planes [2][normed_rows][N]); row r of
+ *                h goes to row out_row[r] (fp32 only) or, with out_row NULL,
+ *                to row r (normed_rows == M). Rows out_row does not name are
+ *                left untouched.
+ *   io           optional (NULL) graph I/O slot: normed is read from io[1]
+ *                when the kernel runs (see dotl_bind_io)
+ *   tile         -1 or 18 (128x256, the one tile built with this epilogue)
+ * Declines (DOTL_DECLINED) for other operand types and for N > 256 or
+ * N % 4 != 0: the caller runs dotl_linear_residual and dotl_layernorm.
+ * Every tensor 16-byte aligned.
+ */
+int dotl_linear_layernorm(const void* x, int x_dtype, const void* w_hi, const float* bias,
+                          const float* residual, float* out, const float* ln_weight,
+                          const float* ln_bias, double eps, void* normed, int normed_dtype,
+                          const int32_t* out_row, int64_t normed_rows, const int64_t* io,
+                          int64_t M, int64_t N, int64_t K, int tile, void* stream);
+
+/*
+ * Zero row r of out (fp32 [rows, width]) wherever row_map[r] < 0: the padded
+ * rows of a padded batch's output, whose valid rows dotl_linear_layernorm
+ * scattered there (row_map is the padded -> packed map, -1 for padding; the
+ * reference zeroes them with masked_fill, optimized/model.py:141-142). With
+ * io, out is read from io[1] when the kernel runs (a graph I/O slot).
+ */
+int dotl_zero_rows(float* out, const int32_t* row_map, int64_t rows, int64_t width,
+                   const int64_t* io, void* stream);
+
+/*
  * Fused scaled-dot-product attention, flash style on MFMA.
  * Replaces fused_attention_forward
  * (reference csrc/attention_dispatch.cuh:332-519).

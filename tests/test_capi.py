@@ -66,7 +66,7 @@ def test_linear_rejects_bad_codes(lib):
     assert lib.dotl_linear_residual(None, 1, None, None, None, None, None, 4, 4, 64, 0, 0, -1,
                                     None) == -1
     # tile ids beyond the menu
-    assert lib.dotl_linear(None, 1, None, None, None, None, 0, 4, 4, 64, 0, 0, 18, None) == -1
+    assert lib.dotl_linear(None, 1, None, None, None, None, 0, 4, 4, 64, 0, 0, 19, None) == -1
     assert b"unknown tile id" in lib.dotl_last_error()
     # empty problems launch nothing and succeed
     assert lib.dotl_linear(None, 0, None, None, None, None, 0, 0, 4, 16, 0, 0, -1, None) == 0
@@ -189,6 +189,45 @@ def test_layernorm_checks(lib):
 def test_bind_io_checks(lib):
     assert lib.dotl_bind_io(None, None, None, None) == -1
     assert b"null slot" in lib.dotl_last_error()
+
+
+def test_linear_layernorm_checks(lib):
+    """The GEMM with the row LayerNorm: argument errors, then declines (1) for
+    what the kernel does not serve, before any device work."""
+    f = lib.dotl_linear_layernorm
+    # normed dtype, scattered rows of a narrowed output, tile menu, extents
+    assert f(None, 1, None, None, None, None, None, None, 1e-5, None, 3, None, 4, None, 4, 64,
+             64, -1, None) == -1
+    assert b"normed output" in lib.dotl_last_error()
+    row = ctypes.c_void_p(16)    # never dereferenced: every call below fails its checks first
+    assert f(None, 1, None, None, None, None, None, None, 1e-5, None, 1, row, 8, None, 4, 64, 64,
+             -1, None) == -1
+    assert b"out_row" in lib.dotl_last_error()
+    assert f(None, 1, None, None, None, None, None, None, 1e-5, None, 0, None, 5, None, 4, 64, 64,
+             -1, None) == -1
+    assert b"rows" in lib.dotl_last_error()
+    assert f(None, 1, None, None, None, None, None, None, 1e-5, None, 0, None, 4, None, 4, 64, 64,
+             15, None) == -1
+    assert b"tile" in lib.dotl_last_error()
+    assert f(None, 1, None, None, None, None, None, None, 1e-5, None, 0, None, -1, None, 4, 64,
+             64, -1, None) == -1
+    # declines: rows wider than a tile, N % 4, K % 64, fp32 x
+    for x_dtype, n, k in ((1, 512, 64), (1, 66, 64), (1, 64, 96), (0, 64, 64)):
+        assert f(None, x_dtype, None, None, None, None, None, None, 1e-5, None, 0, None, 4, None,
+                 4, n, k, -1, None) == 1
+    # empty problems succeed without pointers
+    assert f(None, 1, None, None, None, None, None, None, 1e-5, None, 0, None, 0, None, 0, 64, 64,
+             -1, None) == 0
+    assert f(None, 1, None, None, None, None, None, None, 1e-5, None, 0, None, 4, None, 4, 64, 64,
+             -1, None) == -1
+    assert b"null pointer" in lib.dotl_last_error()
+
+
+def test_zero_rows_checks(lib):
+    assert lib.dotl_zero_rows(None, None, 4, 8, None, None) == -1
+    assert b"null pointer" in lib.dotl_last_error()
+    assert lib.dotl_zero_rows(None, None, -1, 8, None, None) == -1
+    assert lib.dotl_zero_rows(None, None, 0, 8, None, None) == 0
 
 
 def test_mfma_ceiling_probe_checks(lib):

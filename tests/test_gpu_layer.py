@@ -292,21 +292,29 @@ def test_native_library_is_loaded(kernels):
 
 @pytest.mark.parametrize("name", ["C1", "C2", "C3", "C5"])
 def test_residual_epilogue_is_bit_identical(kernels, name):
-    """out_proj and ffn_out adding the residual stream in their epilogues (then
-    plain LayerNorms) give the add+LayerNorm chain's output bit for bit, on the
-    unpadded (C1) and packed-row (C2, C5) paths; no torch fallback runs."""
+    """out_proj and ffn_out adding the residual stream in their epilogues, then
+    plain LayerNorms or (rows of <= 256: C1, C5) the LayerNorms in the same
+    epilogues, give the add+LayerNorm chain's output bit for bit, on the
+    unpadded (C1, C3) and packed-row (C2, C5) paths; no torch fallback runs."""
     cfg = CONFIGS[name]
     x, mask, params = make_case(cfg, batch=min(cfg.batch_size, 64))
-    saved = (ocfg.RESIDUAL_EPILOGUE, ocfg._RESIDUAL_EPILOGUE_MIN_D)
+    saved = (ocfg.RESIDUAL_EPILOGUE, ocfg._RESIDUAL_EPILOGUE_MIN_D, ocfg.LN_EPILOGUE,
+             ocfg._LN_EPILOGUE_MIN_ROWS)
     try:
         outs = {}
         ocfg._RESIDUAL_EPILOGUE_MIN_D = 0   # every width, whatever the default threshold
-        for mode in ("auto", "off"):
-            ocfg.RESIDUAL_EPILOGUE = mode
+        ocfg._LN_EPILOGUE_MIN_ROWS = 0      # every row count, likewise
+        # residual epilogue with the LayerNorms in the same epilogues (C1,
+        # C5: rows of <= 256), with separate LayerNorms, and neither
+        for mode, ln in (("auto", "auto"), ("auto", "off"), ("off", "off")):
+            ocfg.RESIDUAL_EPILOGUE, ocfg.LN_EPILOGUE = mode, ln
             okernels.fallback_counts.clear()
-            outs[mode], _ = _run_gpu(cfg, x, mask, params)
+            outs[(mode, ln)], _ = _run_gpu(cfg, x, mask, params)
             assert not okernels.fallback_counts, dict(okernels.fallback_counts)
     finally:
-        ocfg.RESIDUAL_EPILOGUE, ocfg._RESIDUAL_EPILOGUE_MIN_D = saved
-    assert np.array_equal(outs["auto"], outs["off"])
-    assert compare_outputs(reference_layer(x, mask, params, cfg).numpy(), outs["auto"]).passed
+        (ocfg.RESIDUAL_EPILOGUE, ocfg._RESIDUAL_EPILOGUE_MIN_D, ocfg.LN_EPILOGUE,
+         ocfg._LN_EPILOGUE_MIN_ROWS) = saved
+    assert np.array_equal(outs[("auto", "auto")], outs[("off", "off")])
+    assert np.array_equal(outs[("auto", "off")], outs[("off", "off")])
+    assert compare_outputs(reference_layer(x, mask, params, cfg).numpy(),
+                           outs[("auto", "auto")]).passed
