@@ -207,7 +207,16 @@ def layer_ops(cfg, model, x, mask):
             planes = ln1()
             ln1_bytes = T * D * (8.0 if split else 6.0)
         qkv_w, qkv_b = attn._get_qkv_weight()
-        if split:
+        # an unpadded causal batch keeps the split planes for each sequence's
+        # first rows only (model._split_prefix); the op is then the one-pass
+        # GEMM, the prefix's split GEMM and their two copies
+        prefix = model._split_prefix(x, model._mask_packing(mask)) if split else 0
+        if prefix:
+            planes4 = planes.view(2, B, S, D)
+            qkv_fn = lambda: okernels._linear_bias_split_prefix(  # noqa: E731
+                planes4, qkv_w, qkv_b, True, prefix).view(T, 3 * D)
+            qkv_prec = f"fp16; {qkv_prec} on each sequence's first {prefix} rows"
+        elif split:
             qkv_fn = lambda: kx.linear_bias_split(planes, qkv_w, qkv_b, -1, True,  # noqa: E731
                                                   split_weight=split_w)
         else:
@@ -228,6 +237,9 @@ def layer_ops(cfg, model, x, mask):
         # The model's choice: residual adds in out_proj's and ffn_out's
         # epilogues and plain LayerNorms after them, or add+LayerNorm kernels.
         resid = layer._residual_fused(x2)
+        # rows narrow enough (and many enough) for the LayerNorms in the
+        # out_proj / ffn_out epilogues (optimized.kernels._linear_norm)
+        ln_epi = resid and okernels._ln_epilogue_wanted(R, D)
         if resid:
             attn_out = kx.linear_bias(ctx2, attn.out_proj.weight, attn.out_proj.bias, residual=x2)
             h1 = attn_out
@@ -267,6 +279,34 @@ def layer_ops(cfg, model, x, mask):
         f"linear qkv ({qkv_prec}, fp16 out)": (
             qkv_fn, "mfma", 2.0 * R * D * 3 * D, nb(planes, qkv_b, qkv) + wq16),
         "attention": (attn_fn, "mfma", attention_useful_flops(cfg, L), nb(qkv, ctx) + cu_bytes),
+    }
+    if ln_epi:
+        # out_proj + residual + norm2, ffn_out + residual + the final norm,
+        # each one GEMM (the final one scattering to the padded rows, whose
+        # zeros a second kernel writes)
+        def final_fused():
+            if packing is not None:
+                _, out = kx.linear_layernorm(hidden, layer.ffn_out.weight, layer.ffn_out.bias, h1,
+                                             fw, fb, 1e-5, "float", store_out=False,
+                                             out_row=packing.idx, normed_rows=T)
+                kx.zero_rows(out, packing.inv)
+                return out
+            return kx.linear_layernorm(hidden, layer.ffn_out.weight, layer.ffn_out.bias, h1, fw,
+                                       fb, 1e-5, "float", store_out=False)[1]
+        ops.update({
+            "linear out_proj (+ residual, + norm2 fp16 out)": (
+                lambda: kx.linear_layernorm(ctx2, attn.out_proj.weight, attn.out_proj.bias, x2,
+                                            layer.norm2.weight, layer.norm2.bias, 1e-5, "half"),
+                "mfma", 2.0 * R * D * D, nb(ctx2, x2, h1, n2) + w16(attn.out_proj)),
+            "linear_gelu ffn_in (fp16 out)": (
+                lambda: kx.linear_gelu(n2, layer.ffn_in.weight, layer.ffn_in.bias, -1, -1, True),
+                "mfma", 2.0 * R * D * F, nb(n2, hidden) + w16(layer.ffn_in)),
+            "linear ffn_out (+ residual, + final norm fp32 out)": (
+                final_fused, "mfma", 2.0 * R * F * D,
+                nb(hidden, h1) + T * D * 4.0 + w16(layer.ffn_out)),
+        })
+        return ops
+    ops.update({
         "linear out_proj" + (" (+ residual)" if resid else ""): (
             lambda: kx.linear_bias(ctx2, attn.out_proj.weight, attn.out_proj.bias,
                                    residual=x2 if resid else None),
@@ -287,13 +327,19 @@ def layer_ops(cfg, model, x, mask):
             "mfma", 2.0 * R * F * D, nb(hidden, ffn, h1 if resid else None) + w16(layer.ffn_out)),
         ("layernorm (final, fp32 out)" if resid else "add+layernorm (final, fp32 out)"): (
             final, "hbm", final_bytes, final_bytes),
-    }
+    })
     return ops
 
 
 def final_ln(kt):
-    """The per-kernel table's entry for the layer's last (add+)LayerNorm."""
-    return next(v for k, v in kt.items() if "(final," in k)
+    """The per-kernel table's entry for the layer's last (add+)LayerNorm
+    kernel: the final norm, or norm1 where the final one runs in ffn_out's
+    epilogue."""
+    for tag in ("layernorm (final,", "layernorm (norm1,"):
+        for k, v in kt.items():
+            if k.startswith(tag) or k.startswith("add+" + tag):
+                return v
+    raise KeyError("no LayerNorm kernel in the table")
 
 
 def kernel_table(cfg, model, x, mask, reps):

@@ -76,6 +76,13 @@ _LINEAR_BIAS_MAX_ROWS = 1 << 31
 # projection (half the MFMA work, the 256x256 tiles) runs elsewhere.
 QKV_PRECISION = "auto"
 _QKV_SPLIT_MIN_KEYS = 128
+# Under "auto", an unpadded causal batch with sequences longer than
+# _QKV_SPLIT_MIN_KEYS keeps the split planes only for the rows that attend to
+# fewer keys -- each sequence's first _QKV_SPLIT_MIN_KEYS rows, whose queries
+# see only keys from the same prefix -- and projects the rest in one fp16
+# pass, as the configs whose rows all see >= 128 keys do. C3 (one causal
+# sequence of 4096): the prefix is 3% of the rows.
+_QKV_CAUSAL_PREFIX = True
 # linear_bias `math` when the projection's input is not split planes (an
 # fp32 or fp16 x): the split arithmetic for either split setting.
 _QKV_MATH_CODE = {"fp16x3": 0, "fp16x2": 0, "fp16": -1}

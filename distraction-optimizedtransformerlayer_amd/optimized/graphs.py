@@ -164,7 +164,8 @@ def _graph_key(x: torch.Tensor, use_mask: bool, packing=None) -> Tuple:
             config.RESIDUAL_EPILOGUE, config.LN_EPILOGUE, config.ATTENTION_IMPL, config.LINEAR_GELU,
             config.LINEAR_BIAS, config.LAYERNORM, config.QKV_FP16, config.NORMED_FP16,
             config.CP_ASYNC, config.ATTENTION_PRECISION, config.QKV_PRECISION, config.GELU_FP16,
-            _kernels_mod._stack_precision, _kernels_mod._qkv_few_keys)
+            _kernels_mod._stack_precision, _kernels_mod._qkv_few_keys,
+            _kernels_mod._qkv_split_prefix)
 
 
 def _graph_eligible(x: torch.Tensor, entries: int) -> bool:

@@ -49,6 +49,9 @@ _stack_precision = False
 # attends to fewer than config._QKV_SPLIT_MIN_KEYS keys (what
 # QKV_PRECISION = "auto" resolves on).
 _qkv_few_keys = True
+# Rows of each sequence whose QKV keeps the split arithmetic when only a
+# causal prefix attends to few keys (0: every row, as _qkv_precision says).
+_qkv_split_prefix = 0
 
 
 def _qkv_precision() -> str:
@@ -244,6 +247,25 @@ def _linear_bias_split(planes: torch.Tensor, weight: torch.Tensor, bias: torch.T
     x = planes[0].float() + planes[1].float() / 4096.0
     out = F.linear(x, weight, bias)
     return out.half() if out_half else out
+
+
+def _linear_bias_split_prefix(planes: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
+                              out_half: bool, prefix: int) -> torch.Tensor:
+    """The QKV projection of split planes [2, B, S, D] when only each
+    sequence's first `prefix` rows need the split arithmetic (a causal batch:
+    those rows' queries see only keys of the same prefix): one fp16 pass over
+    every row on the hi plane (the LayerNorm output rounded to fp16, the
+    operand a one-pass projection reads), then the split passes over the
+    prefix rows, written over theirs."""
+    B, S, D = planes.shape[1], planes.shape[2], planes.shape[3]
+    out = _linear_bias(planes[0], weight, bias, out_half=out_half,
+                       math=config._QKV_MATH_CODE["fp16"])
+    # (run on a second stream beside the one-pass GEMM, this small GEMM
+    # measured no faster at C3: 262 us either way, and eager 313)
+    pre = planes[:, :, :prefix].reshape(2, B * prefix, D).contiguous()
+    pre_out = _linear_bias_split(pre, weight, bias, out_half=out_half)
+    out[:, :prefix] = pre_out.view(B, prefix, -1)
+    return out
 
 
 def _layernorm_pack(x: torch.Tensor, norm, packing) -> Tuple[torch.Tensor, torch.Tensor]:

@@ -13,12 +13,14 @@ import torch
 import torch.nn as nn
 
 from . import config
+from . import kernels as okernels
 from .kernels import (_add_layernorm, _add_layernorm_output, _add_layernorm_split,
                       _add_layernorm_unpack,
                       _attention_dispatch, _attention_packed, _attention_wants_fp16,
                       _ffn_block, _ffn_block_eligible, _gelu_input_wants_fp16,
                       _gelu_output_wants_fp16, _layernorm, _layernorm_split,
-                      _linear_bias, _linear_bias_split, _linear_gelu, _linear_norm,
+                      _linear_bias, _linear_bias_split, _linear_bias_split_prefix,
+                      _linear_gelu, _linear_norm,
                       _normed_split_wanted, _normed_wants_fp16, _qkv_math_code,
                       _residual_epilogue_wanted)
 from .util import _version_or_none
@@ -125,7 +127,9 @@ class MySelfAttention(nn.Module):
         # epilogue applies the RNE attention would apply while staging.
         want_half = (_attention_wants_fp16()
                      and config._QKV_FP16_MIN_ROWS <= rows <= config._LINEAR_BIAS_MAX_ROWS)
-        if split:
+        if split and okernels._qkv_split_prefix:
+            qkv = _linear_bias_split_prefix(x, qkv_w, qkv_b, want_half, okernels._qkv_split_prefix)
+        elif split:
             qkv = _linear_bias_split(x, qkv_w, qkv_b, out_half=want_half)
         else:
             qkv = _linear_bias(x, qkv_w, qkv_b, out_half=want_half, math=_qkv_math_code())

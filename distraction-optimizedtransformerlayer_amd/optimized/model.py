@@ -139,13 +139,16 @@ class OptimizedTransformer(nn.Module):
     def forward(self, x: torch.Tensor,
                 valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         stacked = len(self.layers) > 1 and config.STACK_PRECISION == "auto"
-        saved = (okernels._stack_precision, okernels._qkv_few_keys)
+        saved = (okernels._stack_precision, okernels._qkv_few_keys, okernels._qkv_split_prefix)
         okernels._stack_precision = stacked
-        okernels._qkv_few_keys = self._few_key_rows(x, self._mask_packing(valid_token_mask))
+        packing = self._mask_packing(valid_token_mask)
+        okernels._qkv_few_keys = self._few_key_rows(x, packing)
+        okernels._qkv_split_prefix = self._split_prefix(x, packing)
         try:
             return self._forward_dispatch(x, valid_token_mask)
         finally:
-            okernels._stack_precision, okernels._qkv_few_keys = saved
+            (okernels._stack_precision, okernels._qkv_few_keys,
+             okernels._qkv_split_prefix) = saved
 
     def _few_key_rows(self, x: torch.Tensor, packing: Optional[RowPacking]) -> bool:
         """Does some query row attend to fewer than config._QKV_SPLIT_MIN_KEYS
@@ -155,6 +158,18 @@ class OptimizedTransformer(nn.Module):
         if self.config.causal or x.shape[1] < limit:
             return True
         return packing is not None and not packing.trivial and packing.min_len < limit
+
+    def _split_prefix(self, x: torch.Tensor, packing: Optional[RowPacking]) -> int:
+        """Rows of each sequence the split QKV arithmetic is kept for, when
+        only a causal prefix attends to fewer than config._QKV_SPLIT_MIN_KEYS
+        keys (an unpadded causal batch of longer sequences); 0 otherwise."""
+        limit = config._QKV_SPLIT_MIN_KEYS
+        if not (config._QKV_CAUSAL_PREFIX and config.QKV_PRECISION == "auto"
+                and self.config.causal and x.dim() == 3 and x.shape[1] > limit):
+            return 0
+        if packing is not None and not packing.trivial:
+            return 0
+        return limit
 
     def _forward_dispatch(self, x: torch.Tensor,
                           valid_token_mask: Optional[torch.Tensor]) -> torch.Tensor:
