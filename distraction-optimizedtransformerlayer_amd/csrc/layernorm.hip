@@ -440,8 +440,10 @@ extern "C" int dotl_bind_io(int64_t* slot, const void* in, void* out, void* stre
     return check_launch("bind_io");
 }
 
-// Zero rows of a padded output: one wave per row, rows with row_map[r] >= 0
-// (written by the producer) left alone.
+// Zero rows of a padded output, rows with row_map[r] >= 0 (written by the
+// producer) left alone. Each wave reads the map entries of 64 rows at once
+// (one a lane) and then stores zeros to the padded ones back to back: with a
+// wave per row, every row first waited out its own map load.
 namespace dotl {
 namespace {
 __global__ __launch_bounds__(256) void zero_rows_kernel(float* __restrict__ out,
@@ -450,16 +452,22 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(float* __restrict__ out,
                                                         const int64_t* __restrict__ io) {
     if (io != nullptr) out = reinterpret_cast<float*>(io[1]);
     const int lane = threadIdx.x & 63;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kRowsPerBlock;
-    for (int64_t r = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-         r < rows; r += stride) {
-        if (row_map[r] >= 0) continue;   // wave-uniform
-        float* row = out + r * width;
-        if ((width & 3) == 0) {
-            for (int64_t c = 4 * lane; c < width; c += 256)
-                *reinterpret_cast<float4*>(row + c) = make_float4(0.f, 0.f, 0.f, 0.f);
-        } else {
-            for (int64_t c = lane; c < width; c += 64) row[c] = 0.f;
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * kRowsPerBlock;
+    for (int64_t r0 = (static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6)) * 64;
+         r0 < rows; r0 += waves * 64) {
+        const int64_t r = r0 + lane;
+        const bool pad = r < rows && row_map[r] < 0;
+        uint64_t todo = __ballot(pad);
+        while (todo != 0) {   // wave-uniform
+            const int i = __builtin_ctzll(todo);
+            todo &= todo - 1;
+            float* row = out + (r0 + i) * width;
+            if ((width & 3) == 0) {
+                for (int64_t c = 4 * lane; c < width; c += 256)
+                    *reinterpret_cast<float4*>(row + c) = make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+                for (int64_t c = lane; c < width; c += 64) row[c] = 0.f;
+            }
         }
     }
 }
@@ -474,7 +482,7 @@ extern "C" int dotl_zero_rows(float* out, const int32_t* row_map, int64_t rows, 
     if (rows == 0 || width == 0) return DOTL_OK;
     DOTL_REQUIRE((out || io) && row_map, "zero_rows: null pointer");
     DOTL_REQUIRE(reinterpret_cast<uintptr_t>(out) % 16 == 0, "zero_rows: out must be 16-byte aligned");
-    hipLaunchKernelGGL(zero_rows_kernel, dim3(grid_for(rows)), dim3(256), 0, as_stream(stream), out,
-                       row_map, rows, width, io);
+    hipLaunchKernelGGL(zero_rows_kernel, dim3(grid_for((rows + 63) / 64)), dim3(256), 0,
+                       as_stream(stream), out, row_map, rows, width, io);
     return check_launch("zero_rows");
 }
