@@ -438,9 +438,12 @@ extern "C" int dotl_weight_split(const float* w, void* w_hi, void* w_lo, int64_t
 namespace dotl {
 namespace {
 
+// x_lo: the lo plane of a split x (DOTL_F16X2) where it does not follow the
+// hi plane directly (null: at x + M * K).
 int linear_impl(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
                 const float* bias, const float* residual, void* out, int out_dtype, int64_t M,
-                int64_t N, int64_t K, int act, int math, int tile, void* stream) {
+                int64_t N, int64_t K, int act, int math, int tile, void* stream,
+                const void* x_lo = nullptr) {
     clear_error();
     const char* who = act == DOTL_ACT_GELU ? "linear_gelu" : "linear_bias";
     DOTL_REQUIRE(x_dtype == DOTL_F32 || x_dtype == DOTL_F16 || x_dtype == DOTL_F16X2 ||
@@ -487,7 +490,9 @@ int linear_impl(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
     const bool dma_fits = M * K * 2 < (int64_t{1} << 32) && N * K * 2 < (int64_t{1} << 32);
     if (!force_staged && x_dtype != DOTL_F32 && K % 64 == 0 && dma_fits) {
         const _Float16* xh = static_cast<const _Float16*>(x);
-        const _Float16* xl = x_dtype == DOTL_F16X2 ? xh + M * K : nullptr;
+        const _Float16* xl =
+            x_dtype != DOTL_F16X2 ? nullptr
+                                  : (x_lo != nullptr ? static_cast<const _Float16*>(x_lo) : xh + M * K);
         // split modes: bit 0 lo(W), bit 1 lo(x)
         const int mode = bf16 ? 4
                          : (math == DOTL_MATH_FP16X2 ? 2
@@ -539,6 +544,21 @@ extern "C" int dotl_linear(const void* x, int x_dtype, const void* w_hi, const v
                            int64_t K, int act, int math, int tile, void* stream) {
     return dotl::linear_impl(x, x_dtype, w_hi, w_lo, bias, nullptr, out, out_dtype, M, N, K, act,
                              math, tile, stream);
+}
+
+extern "C" int dotl_linear_planes(const void* x_hi, const void* x_lo, const void* w_hi,
+                                  const void* w_lo, const float* bias, void* out, int out_dtype,
+                                  int64_t M, int64_t N, int64_t K, int math, int tile,
+                                  void* stream) {
+    using namespace dotl;
+    clear_error();
+    DOTL_REQUIRE(M == 0 || N == 0 || x_lo != nullptr, "linear_bias: null lo plane");
+    DOTL_REQUIRE(reinterpret_cast<uintptr_t>(x_lo) % 16 == 0,
+                 "linear_bias: the lo plane must be 16-byte aligned");
+    DOTL_REQUIRE(math == DOTL_MATH_FP16X2 || math == DOTL_MATH_FP16X3,
+                 "linear_bias: split planes take the fp16x2 or fp16x3 math");
+    return linear_impl(x_hi, DOTL_F16X2, w_hi, w_lo, bias, nullptr, out, out_dtype, M, N, K,
+                       DOTL_ACT_NONE, math, tile, stream, x_lo);
 }
 
 extern "C" int dotl_linear_residual(const void* x, int x_dtype, const void* w_hi,

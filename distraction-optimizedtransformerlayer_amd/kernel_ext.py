@@ -61,6 +61,7 @@ EXPORTED_SYMBOLS = (
     "dotl_attention_split_plan", "dotl_wmma_set_split_kv", "dotl_wmma_split_kv_enabled",
     "dotl_wmma_set_split_count", "dotl_attention_forward_noalloc",
     "dotl_attention_noalloc_scratch_bytes", "dotl_linear_layernorm", "dotl_zero_rows",
+    "dotl_linear_planes",
 )
 
 _kernels = None
@@ -118,6 +119,8 @@ def _declare(lib) -> None:
     lib.dotl_linear_residual.restype = i32
     lib.dotl_linear_residual.argtypes = [vp, i32, vp, vp, vp, vp, vp, i64, i64, i64, i32, i32,
                                          i32, vp]
+    lib.dotl_linear_planes.restype = i32
+    lib.dotl_linear_planes.argtypes = [vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i32, i32, vp]
     lib.dotl_linear_layernorm.restype = i32
     lib.dotl_linear_layernorm.argtypes = [vp, i32, vp, vp, vp, vp, vp, vp, c.c_double, vp, i32,
                                           vp, i64, vp, i64, i64, i64, i32, vp]
@@ -691,6 +694,34 @@ class Kernels:
             bias.contiguous().data_ptr(), out.data_ptr(), DOTL_F16 if out_half else DOTL_F32,
             M, N, K, DOTL_ACT_NONE, DOTL_MATH_FP16X3 if split_weight else DOTL_MATH_FP16X2,
             int(tile), self._stream(pc.device)))
+        if rc == DOTL_DECLINED:
+            return None
+        return out
+
+    def linear_bias_planes(self, hi, lo, weight, bias, out, split_weight=False):
+        """linear_bias_split with the two planes as separate [M, K] fp16
+        tensors (each contiguous; e.g. a block of rows of a [2, rows, K]
+        LayerNorm output) and the result written into `out` ([M, N], fp16 or
+        fp32, contiguous; e.g. a block of rows of a larger output). Not in
+        the reference's surface. Returns `out`, or None where declined."""
+        import torch
+
+        who = "linear_bias"
+        self._require_cuda(who, hi, lo, weight, bias, out)
+        K, N = weight.shape[1], weight.shape[0]
+        if (hi.dtype != torch.float16 or lo.dtype != torch.float16 or hi.shape != lo.shape
+                or hi.shape[-1] != K or not hi.is_contiguous() or not lo.is_contiguous()):
+            raise RuntimeError(f"{who}: hi and lo must be contiguous float16 [M, {K}] planes")
+        M = hi.numel() // K
+        if (out.dtype not in (torch.float16, torch.float32) or not out.is_contiguous()
+                or out.numel() != M * N):
+            raise RuntimeError(f"{who}: out must be a contiguous float16/float32 [{M}, {N}]")
+        whi, wlo = self.weight_half(weight, bool(split_weight))
+        rc = self._check(self._lib.dotl_linear_planes(
+            hi.data_ptr(), lo.data_ptr(), whi.data_ptr(), wlo.data_ptr() if wlo is not None else None,
+            bias.contiguous().data_ptr(), out.data_ptr(),
+            DOTL_F16 if out.dtype == torch.float16 else DOTL_F32, M, N, K,
+            DOTL_MATH_FP16X3 if split_weight else DOTL_MATH_FP16X2, -1, self._stream(hi.device)))
         if rc == DOTL_DECLINED:
             return None
         return out

@@ -262,6 +262,15 @@ def _linear_bias_split_prefix(planes: torch.Tensor, weight: torch.Tensor, bias: 
                        math=config._QKV_MATH_CODE["fp16"])
     # (run on a second stream beside the one-pass GEMM, this small GEMM
     # measured no faster at C3: 262 us either way, and eager 313)
+    kernels = _custom_kernels()
+    if B == 1 and kernels is not None and planes.is_contiguous() and out.is_contiguous():
+        # one sequence: its prefix rows are contiguous in both planes and in
+        # the output, so the split GEMM reads and writes them in place
+        done = kernels.linear_bias_planes(planes[0, 0, :prefix], planes[1, 0, :prefix], weight,
+                                          bias, out[0, :prefix],
+                                          split_weight=_qkv_precision() == "fp16x3")
+        if done is not None:
+            return out
     pre = planes[:, :, :prefix].reshape(2, B * prefix, D).contiguous()
     pre_out = _linear_bias_split(pre, weight, bias, out_half=out_half)
     out[:, :prefix] = pre_out.view(B, prefix, -1)

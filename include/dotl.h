@@ -209,6 +209,20 @@ int dotl_linear_residual(const void* x, int x_dtype, const void* w_hi, const voi
                          int64_t N, int64_t K, int act, int math, int tile, void* stream);
 
 /*
+ * dotl_linear on split fp16 planes (x_dtype DOTL_F16X2) whose lo plane does
+ * not directly follow the hi plane: x_hi and x_lo each fp16 [M, K]
+ * (contiguous, 16-byte aligned), e.g. a block of rows of a [2][rows][K]
+ * LayerNorm output; no activation; math DOTL_MATH_FP16X2 or
+ * DOTL_MATH_FP16X3. Otherwise as dotl_linear (reference linear_bias,
+ * csrc/linear_gelu.cuh:598-719, whose input here is the split form). No
+ * counterpart entry in the reference: the layer projects one causal
+ * prefix's rows this way, in place, into the QKV output.
+ */
+int dotl_linear_planes(const void* x_hi, const void* x_lo, const void* w_hi, const void* w_lo,
+                       const float* bias, void* out, int out_dtype, int64_t M, int64_t N,
+                       int64_t K, int math, int tile, void* stream);
+
+/*
  * h = residual + x @ W^T + bias (fp32 [M, N]) and normed = LayerNorm(h) *
  * ln_weight + ln_bias in one kernel: linear_bias followed by the reference's
  * fused_add_layernorm (csrc/linear_gelu.cuh:598-719, then

@@ -223,6 +223,25 @@ def test_linear_layernorm_checks(lib):
     assert b"null pointer" in lib.dotl_last_error()
 
 
+def test_linear_planes_checks(lib):
+    """Split planes given apart: the lo plane and the math are checked before
+    the shared linear checks, all before any device work."""
+    f = lib.dotl_linear_planes
+    assert f(None, None, None, None, None, None, 0, 4, 64, 64, 1, -1, None) == -1
+    assert b"lo plane" in lib.dotl_last_error()
+    assert f(None, ctypes.c_void_p(8), None, None, None, None, 0, 4, 64, 64, 1, -1, None) == -1
+    assert b"aligned" in lib.dotl_last_error()
+    lo = ctypes.c_void_p(16)     # never dereferenced: every call below fails its checks first
+    assert f(None, lo, None, None, None, None, 0, 4, 64, 64, 0, -1, None) == -1
+    assert b"fp16x2 or fp16x3" in lib.dotl_last_error()
+    assert f(None, lo, None, None, None, None, 0, 4, 64, 96, 2, -1, None) == 1   # K % 64
+    assert f(None, lo, None, None, None, None, 0, 4, 64, 64, 1, -1, None) == -1
+    assert b"split weight" in lib.dotl_last_error()
+    assert f(None, lo, None, None, None, None, 0, 4, 64, 64, 2, -1, None) == -1
+    assert b"null pointer" in lib.dotl_last_error()
+    assert f(None, None, None, None, None, None, 0, 0, 64, 64, 2, -1, None) == 0
+
+
 def test_zero_rows_checks(lib):
     assert lib.dotl_zero_rows(None, None, 4, 8, None, None) == -1
     assert b"null pointer" in lib.dotl_last_error()

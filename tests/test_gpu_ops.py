@@ -481,6 +481,31 @@ def test_gemm_dma_split_planes(kernels, M, N, K, tile, act):
         np.testing.assert_allclose(got.cpu().numpy(), want, atol=3e-6 * np.sqrt(K / 128), rtol=2e-6)
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 768, 256), (300, 200, 128), (513, 384, 64)])
+@pytest.mark.parametrize("half_out", [False, True])
+@pytest.mark.parametrize("split_weight", [False, True])
+def test_gemm_planes_in_place(kernels, M, N, K, half_out, split_weight):
+    """linear_bias_planes: the first M rows of [2, rows, K] planes, read in
+    place, written into the first M rows of a larger output, equal
+    linear_bias_split on a compacted copy of those rows bit for bit; the
+    output's other rows are untouched."""
+    rows = M + 77
+    x, w, b = _gemm_case(rows, N, K, 13 * M + N)
+    xt = _t(x)
+    hi = xt.half()
+    lo = ((xt - hi.float()) * 4096.0).half()
+    planes = torch.stack([hi, lo])
+    want = kernels.linear_bias_split(planes[:, :M].contiguous(), _t(w), _t(b), -1, half_out,
+                                     split_weight=split_weight)
+    out = torch.full((rows, N), 7.0, device=DEV, dtype=torch.float16 if half_out else torch.float32)
+    got = kernels.linear_bias_planes(planes[0, :M], planes[1, :M], _t(w), _t(b), out[:M],
+                                     split_weight=split_weight)
+    assert got is not None and got.data_ptr() == out.data_ptr()
+    torch.cuda.synchronize()
+    assert torch.equal(out[:M], want)
+    assert bool((out[M:] == 7.0).all())
+
+
 @pytest.mark.parametrize("M,N,K", DMA_SHAPES)
 @pytest.mark.parametrize("tile", [-1, 3, 5, 9, 10, 12, 13, 15, 16, 17])
 def test_gemm_residual_epilogue(kernels, M, N, K, tile):
