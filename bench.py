@@ -293,11 +293,29 @@ def layer_ops(cfg, model, x, mask):
                 return out
             return kx.linear_layernorm(hidden, layer.ffn_out.weight, layer.ffn_out.bias, h1, fw,
                                        fb, 1e-5, "float", store_out=False)[1]
+        ops["linear out_proj (+ residual, + norm2 fp16 out)"] = (
+            lambda: kx.linear_layernorm(ctx2, attn.out_proj.weight, attn.out_proj.bias, x2,
+                                        layer.norm2.weight, layer.norm2.bias, 1e-5, "half"),
+            "mfma", 2.0 * R * D * D, nb(ctx2, x2, h1, n2) + w16(attn.out_proj))
+        if okernels._ffn_ln_wanted(n2, layer.ffn_in, layer.ffn_out):
+            # the whole FFN with the residual add and the final norm, one
+            # kernel (optimized.kernels._ffn_norm)
+            def ffn_fused():
+                if packing is not None:
+                    _, out = kx.ffn_layernorm(n2, layer.ffn_in.weight, layer.ffn_in.bias,
+                                              layer.ffn_out.weight, layer.ffn_out.bias, h1, fw,
+                                              fb, 1e-5, "float", out_row=packing.idx,
+                                              normed_rows=T)
+                    kx.zero_rows(out, packing.inv)
+                    return out
+                return kx.ffn_layernorm(n2, layer.ffn_in.weight, layer.ffn_in.bias,
+                                        layer.ffn_out.weight, layer.ffn_out.bias, h1, fw, fb,
+                                        1e-5, "float")[1]
+            ops["ffn (ffn_in, GELU, ffn_out, + residual, + final norm fp32 out)"] = (
+                ffn_fused, "mfma", 4.0 * R * D * F,
+                nb(n2, h1) + T * D * 4.0 + w16(layer.ffn_in) + w16(layer.ffn_out))
+            return ops
         ops.update({
-            "linear out_proj (+ residual, + norm2 fp16 out)": (
-                lambda: kx.linear_layernorm(ctx2, attn.out_proj.weight, attn.out_proj.bias, x2,
-                                            layer.norm2.weight, layer.norm2.bias, 1e-5, "half"),
-                "mfma", 2.0 * R * D * D, nb(ctx2, x2, h1, n2) + w16(attn.out_proj)),
             "linear_gelu ffn_in (fp16 out)": (
                 lambda: kx.linear_gelu(n2, layer.ffn_in.weight, layer.ffn_in.bias, -1, -1, True),
                 "mfma", 2.0 * R * D * F, nb(n2, hidden) + w16(layer.ffn_in)),

@@ -152,27 +152,42 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// A value the compiler must treat as computed: narrowing it cannot be fused
+// into the multiply-add that produced it. Left free, the backend may turn
+// fp32 fma + fp16 conversion into one v_fma_mixlo_f16 (a single rounding to
+// fp16), which differs in the last fp16 bit from the fp32 result narrowed
+// with RNE -- the arithmetic the reference and every other kernel here use --
+// and whether it does depends on the surrounding code.
+__device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
+
 // erf GELU, 0.5 x (1 + erf(x / sqrt 2)), with erf from Abramowitz &
 // Stegun, Handbook of Mathematical Functions, formula 7.1.26:
 //   erfc(z) ~= (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),
 //   t = 1 / (1 + p z), z >= 0, |error in erf| <= 1.5e-7.
 // Written on erfc so neither sign cancels: with z = |x| / sqrt 2 and
-// q = erfc(z), GELU(x) = x - x q / 2 for x >= 0 and x q / 2 for x < 0.
-// One reciprocal, one exp2 and seven FMAs; the device library's erff costs
-// several times that, and an epilogue that applies it to every output of a
-// GEMM with a short K spends more time there than in the MFMAs.
+// q = erfc(z), GELU(x) = x - |x| q / 2 for x >= 0 and -|x| q / 2 for x < 0,
+// i.e. max(x, 0) + (-q / 2) |x|, one fma. The -1/2 is folded into the
+// coefficients (a power of two: the Horner steps round exactly as before,
+// scaled). |x| is clamped at 2^64 in that product so that x = +-inf, where
+// q = 0, gives inf and 0 rather than 0 * inf. One reciprocal, one exp2 and
+// nine other operations; the device library's erff costs several times that,
+// and an epilogue that applies it to every output of a GEMM with a short K
+// spends more time there than in the MFMAs.
 __device__ __forceinline__ float gelu_erf(float x) {
-    const float z = fabsf(x) * 0.70710678118654752440f;
+    const float ax = fabsf(x);
+    const float z = ax * 0.70710678118654752440f;
     const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
-    float poly = fmaf(1.061405429f, t, -1.453152027f);
-    poly = fmaf(poly, t, 1.421413741f);
-    poly = fmaf(poly, t, -0.284496736f);
-    poly = fmaf(poly, t, 0.254829592f);
+    float poly = fmaf(-0.5307027145f, t, 0.7265760135f);     // -a5 / 2, -a4 / 2
+    poly = fmaf(poly, t, -0.7107068705f);                     // -a3 / 2
+    poly = fmaf(poly, t, 0.142248368f);                       // -a2 / 2
+    poly = fmaf(poly, t, -0.127414796f);                      // -a1 / 2
     poly *= t;
-    // exp(-z^2) = exp2(-z^2 log2 e)
-    const float q = poly * __builtin_amdgcn_exp2f(-z * z * 1.44269504088896341f);
-    const float h = q == 0.f ? 0.f : 0.5f * x * q;  // q == 0 at |x| = inf
-    return x >= 0.f ? x - h : h;
+    // exp(-z^2) = exp2(-x^2 log2(e) / 2)
+    const float hq = poly * __builtin_amdgcn_exp2f(x * (x * -0.72134752044448170368f));
+    // opaque: an fp16 output is this fp32 value narrowed, in every kernel
+    float g = fmaf(hq, fminf(ax, 0x1p64f), fmaxf(x, 0.f));
+    opaque(g);
+    return g;
 }
 
 // LayerNorm arithmetic shared by every kernel that normalises a row, each
@@ -214,13 +229,6 @@ template <> struct normed_type<DOTL_F16> { using type = _Float16; };
 template <> struct normed_type<DOTL_F16X2> { using type = _Float16; };
 template <> struct normed_type<DOTL_BF16> { using type = __bf16; };
 
-// A value the compiler must treat as computed: narrowing it cannot be fused
-// into the multiply-add that produced it. Left free, the backend may turn
-// fp32 fma + fp16 conversion into one v_fma_mixlo_f16 (a single rounding to
-// fp16), which differs in the last fp16 bit from the fp32 result narrowed
-// with RNE -- the arithmetic the reference and every other kernel here use --
-// and whether it does depends on the surrounding code.
-__device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
 
 // Four normalised values to a LayerNorm's normed output (split planes: hi,
 // then lo in the second plane, `plane` elements further on).

@@ -331,125 +331,14 @@ struct DmaGemm {
     }
 };
 
-// LN >= 0: the row LayerNorm epilogue (LnEpi; LN & 3 the normed dtype code,
-// LN & 4 set when C is stored as well).
-template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT, int NWV = 4, int LN = -1>
-__global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
-    const _Float16* __restrict__ A, const _Float16* __restrict__ Alo,
-    const _Float16* __restrict__ W, const _Float16* __restrict__ Wlo,
-    const float* __restrict__ bias, const float* __restrict__ R, void* __restrict__ C, int64_t M,
-    int64_t N, int64_t K, LnEpi ln) {
-    using G = DmaGemm<BM, BN, BK, NS, MODE, ACT, OUTT, NWV>;
-    using L = typename G::L;
-    static_assert(NS >= 2 && NS <= 8, "2 to 8 stages");
-    static_assert((NS - 2) * L::LOADS < 64, "vmcnt is 6 bits");
-    constexpr int SZ = L::HALVES;
-
-    // One __shared__ array per stage (see the header comment).
-    __shared__ __attribute__((aligned(1024))) _Float16 st0[SZ];
-    __shared__ __attribute__((aligned(1024))) _Float16 st1[SZ];
-    __shared__ __attribute__((aligned(1024))) _Float16 st2[NS > 2 ? SZ : 8];
-    __shared__ __attribute__((aligned(1024))) _Float16 st3[NS > 3 ? SZ : 8];
-    __shared__ __attribute__((aligned(1024))) _Float16 st4[NS > 4 ? SZ : 8];
-    __shared__ __attribute__((aligned(1024))) _Float16 st5[NS > 5 ? SZ : 8];
-    __shared__ __attribute__((aligned(1024))) _Float16 st6[NS > 6 ? SZ : 8];
-    __shared__ __attribute__((aligned(1024))) _Float16 st7[NS > 7 ? SZ : 8];
-
-    G g;
-    g.A = A; g.Alo = Alo; g.W = W; g.Wlo = Wlo;
-    g.M = M; g.N = N; g.K = K;
-    g.lane = threadIdx.x & 63;
-    g.wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    g.wm = g.wave / G::WGN;
-    g.wn = g.wave % G::WGN;
-    g.lr = g.lane & 31;
-    g.lg = g.lane >> 5;
-    int64_t mt, nt;
-    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, mt, nt);
-    g.m0 = mt * BM;
-    g.n0 = nt * BN;
-    g.nk = K / BK;
-    g.init_offsets();
-#pragma unroll
-    for (int i = 0; i < G::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < G::TN; ++j) {
-            g.acc[i][j] = floatx16{};
-            if constexpr (G::SPLIT) g.acc2[i][j] = floatx16{};
-        }
-
-    auto stage = [&](auto s) -> _Float16* {
-        constexpr int S = decltype(s)::value;
-        if constexpr (S == 0) return st0;
-        else if constexpr (S == 1) return st1;
-        else if constexpr (S == 2) return st2;
-        else if constexpr (S == 3) return st3;
-        else if constexpr (S == 4) return st4;
-        else if constexpr (S == 5) return st5;
-        else if constexpr (S == 6) return st6;
-        else return st7;
-    };
-
-    // The tile's bias columns, staged in LDS before the K loop (the loop's
-    // barriers publish them): read in the epilogue from LDS, they do not wait
-    // behind the epilogue's own global stores the way a global load would.
-    __shared__ __attribute__((aligned(16))) float sbias[BN];
-    for (int c = threadIdx.x; c < BN; c += NWV * 64) {
-        const int64_t col = g.n0 + c;
-        sbias[c] = col < N ? bias[col] : 0.f;
-    }
-
-    // Prologue: tiles 0 .. NS-2 in flight.
-    auto prologue = [&](auto s) {
-        constexpr int S = decltype(s)::value;
-        if constexpr (S < NS - 1) {
-            if (S < g.nk) g.template issue_range<0, G::NDMA>(stage(s), S);
-        }
-    };
-    prologue(std::integral_constant<int, 0>{});
-    prologue(std::integral_constant<int, 1>{});
-    prologue(std::integral_constant<int, 2>{});
-    prologue(std::integral_constant<int, 3>{});
-    prologue(std::integral_constant<int, 4>{});
-    prologue(std::integral_constant<int, 5>{});
-    prologue(std::integral_constant<int, 6>{});
-
-    // One step: wait for tile kt (in stage S), barrier (everyone's DMAs for kt
-    // landed, everyone done reading the stage tile kt + NS - 1 will reuse),
-    // multiply tile kt while issuing tile kt + NS - 1 into stage
-    // (S + NS - 1) % NS.
-    auto step = [&](auto s, int64_t kt) {
-        constexpr int S = decltype(s)::value;
-        if constexpr (S < NS) {
-            constexpr int NEXT = (S + NS - 1) % NS;
-            g.wait_tile(kt);
-            stage_barrier();
-            g.compute(stage(s), stage(std::integral_constant<int, NEXT>{}), kt + NS - 1,
-                      kt + NS - 1 < g.nk, kt > 0);
-        }
-    };
-
-    int64_t kt = 0;
-    for (; kt + NS <= g.nk; kt += NS) {
-        step(std::integral_constant<int, 0>{}, kt);
-        step(std::integral_constant<int, 1>{}, kt + 1);
-        step(std::integral_constant<int, 2>{}, kt + 2);
-        step(std::integral_constant<int, 3>{}, kt + 3);
-        step(std::integral_constant<int, 4>{}, kt + 4);
-        step(std::integral_constant<int, 5>{}, kt + 5);
-        step(std::integral_constant<int, 6>{}, kt + 6);
-        step(std::integral_constant<int, 7>{}, kt + 7);
-    }
-    // Remainder: fewer than NS tiles, in stages 0, 1, ...
-    if (kt < g.nk) step(std::integral_constant<int, 0>{}, kt);
-    if (kt + 1 < g.nk) step(std::integral_constant<int, 1>{}, kt + 1);
-    if (kt + 2 < g.nk) step(std::integral_constant<int, 2>{}, kt + 2);
-    if (kt + 3 < g.nk) step(std::integral_constant<int, 3>{}, kt + 3);
-    if (kt + 4 < g.nk) step(std::integral_constant<int, 4>{}, kt + 4);
-    if (kt + 5 < g.nk) step(std::integral_constant<int, 5>{}, kt + 5);
-    if (kt + 6 < g.nk) step(std::integral_constant<int, 6>{}, kt + 6);
-    g.finish();   // the last tile's deferred MFMAs
-
+// The tile's epilogue, shared by the pipelined GEMM and the fused FFN
+// kernel: bias, activation, residual and the row LayerNorm applied to the
+// accumulators of G (a DmaGemm), and the stores. stage_buf(b) returns LDS
+// stage buffer b (0 <= b < NS) of SZ halves each, free once the K loop ends.
+template <int BM, int BN, int NS, int ACT, int OUTT, int NWV, int LN, int SZ, class G, class BufFn>
+__device__ __forceinline__ void store_tile(G& g, BufFn stage_buf, const float* sbias,
+                                           const float* __restrict__ R, void* __restrict__ C,
+                                           int64_t M, int64_t N, const LnEpi& ln) {
     // Epilogue. The MFMAs were issued as W x A^T, so each 32x32 accumulator
     // holds a tile of C^T: lane l owns C row (l % 32) of the tile, and
     // registers 4g .. 4g+3 hold the four consecutive C columns
@@ -529,17 +418,7 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
     constexpr int RR = RPB * NS;                            // tile rows a round holds
     constexpr int ROUNDS = (BM + RR - 1) / RR;
     constexpr int THREADS = NWV * 64;
-    auto buf = [&](int b) -> float* {
-        _Float16* p = st0;
-        if (b == 1) p = st1;
-        if constexpr (NS > 2) if (b == 2) p = st2;
-        if constexpr (NS > 3) if (b == 3) p = st3;
-        if constexpr (NS > 4) if (b == 4) p = st4;
-        if constexpr (NS > 5) if (b == 5) p = st5;
-        if constexpr (NS > 6) if (b == 6) p = st6;
-        if constexpr (NS > 7) if (b == 7) p = st7;
-        return reinterpret_cast<float*>(p);
-    };
+    auto buf = [&](int b) -> float* { return reinterpret_cast<float*>(stage_buf(b)); };
     // The LayerNorm epilogue: a wave instruction covers one row (64 lanes x
     // 4 columns), so each lane's columns are the same in every row; their
     // weights are loaded once.
@@ -781,6 +660,139 @@ __global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
     else
         rounds(std::integral_constant<int, 0>{});
     }
+}
+
+// LN >= 0: the row LayerNorm epilogue (LnEpi; LN & 3 the normed dtype code,
+// LN & 4 set when C is stored as well).
+template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT, int NWV = 4, int LN = -1>
+__global__ __launch_bounds__(NWV * 64) void gemm_dma_kernel(
+    const _Float16* __restrict__ A, const _Float16* __restrict__ Alo,
+    const _Float16* __restrict__ W, const _Float16* __restrict__ Wlo,
+    const float* __restrict__ bias, const float* __restrict__ R, void* __restrict__ C, int64_t M,
+    int64_t N, int64_t K, LnEpi ln) {
+    using G = DmaGemm<BM, BN, BK, NS, MODE, ACT, OUTT, NWV>;
+    using L = typename G::L;
+    static_assert(NS >= 2 && NS <= 8, "2 to 8 stages");
+    static_assert((NS - 2) * L::LOADS < 64, "vmcnt is 6 bits");
+    constexpr int SZ = L::HALVES;
+
+    // One __shared__ array per stage (see the header comment).
+    __shared__ __attribute__((aligned(1024))) _Float16 st0[SZ];
+    __shared__ __attribute__((aligned(1024))) _Float16 st1[SZ];
+    __shared__ __attribute__((aligned(1024))) _Float16 st2[NS > 2 ? SZ : 8];
+    __shared__ __attribute__((aligned(1024))) _Float16 st3[NS > 3 ? SZ : 8];
+    __shared__ __attribute__((aligned(1024))) _Float16 st4[NS > 4 ? SZ : 8];
+    __shared__ __attribute__((aligned(1024))) _Float16 st5[NS > 5 ? SZ : 8];
+    __shared__ __attribute__((aligned(1024))) _Float16 st6[NS > 6 ? SZ : 8];
+    __shared__ __attribute__((aligned(1024))) _Float16 st7[NS > 7 ? SZ : 8];
+
+    G g;
+    g.A = A; g.Alo = Alo; g.W = W; g.Wlo = Wlo;
+    g.M = M; g.N = N; g.K = K;
+    g.lane = threadIdx.x & 63;
+    g.wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    g.wm = g.wave / G::WGN;
+    g.wn = g.wave % G::WGN;
+    g.lr = g.lane & 31;
+    g.lg = g.lane >> 5;
+    int64_t mt, nt;
+    tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, mt, nt);
+    g.m0 = mt * BM;
+    g.n0 = nt * BN;
+    g.nk = K / BK;
+    g.init_offsets();
+#pragma unroll
+    for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j) {
+            g.acc[i][j] = floatx16{};
+            if constexpr (G::SPLIT) g.acc2[i][j] = floatx16{};
+        }
+
+    auto stage = [&](auto s) -> _Float16* {
+        constexpr int S = decltype(s)::value;
+        if constexpr (S == 0) return st0;
+        else if constexpr (S == 1) return st1;
+        else if constexpr (S == 2) return st2;
+        else if constexpr (S == 3) return st3;
+        else if constexpr (S == 4) return st4;
+        else if constexpr (S == 5) return st5;
+        else if constexpr (S == 6) return st6;
+        else return st7;
+    };
+
+    // The tile's bias columns, staged in LDS before the K loop (the loop's
+    // barriers publish them): read in the epilogue from LDS, they do not wait
+    // behind the epilogue's own global stores the way a global load would.
+    __shared__ __attribute__((aligned(16))) float sbias[BN];
+    for (int c = threadIdx.x; c < BN; c += NWV * 64) {
+        const int64_t col = g.n0 + c;
+        sbias[c] = col < N ? bias[col] : 0.f;
+    }
+
+    // Prologue: tiles 0 .. NS-2 in flight.
+    auto prologue = [&](auto s) {
+        constexpr int S = decltype(s)::value;
+        if constexpr (S < NS - 1) {
+            if (S < g.nk) g.template issue_range<0, G::NDMA>(stage(s), S);
+        }
+    };
+    prologue(std::integral_constant<int, 0>{});
+    prologue(std::integral_constant<int, 1>{});
+    prologue(std::integral_constant<int, 2>{});
+    prologue(std::integral_constant<int, 3>{});
+    prologue(std::integral_constant<int, 4>{});
+    prologue(std::integral_constant<int, 5>{});
+    prologue(std::integral_constant<int, 6>{});
+
+    // One step: wait for tile kt (in stage S), barrier (everyone's DMAs for kt
+    // landed, everyone done reading the stage tile kt + NS - 1 will reuse),
+    // multiply tile kt while issuing tile kt + NS - 1 into stage
+    // (S + NS - 1) % NS.
+    auto step = [&](auto s, int64_t kt) {
+        constexpr int S = decltype(s)::value;
+        if constexpr (S < NS) {
+            constexpr int NEXT = (S + NS - 1) % NS;
+            g.wait_tile(kt);
+            stage_barrier();
+            g.compute(stage(s), stage(std::integral_constant<int, NEXT>{}), kt + NS - 1,
+                      kt + NS - 1 < g.nk, kt > 0);
+        }
+    };
+
+    int64_t kt = 0;
+    for (; kt + NS <= g.nk; kt += NS) {
+        step(std::integral_constant<int, 0>{}, kt);
+        step(std::integral_constant<int, 1>{}, kt + 1);
+        step(std::integral_constant<int, 2>{}, kt + 2);
+        step(std::integral_constant<int, 3>{}, kt + 3);
+        step(std::integral_constant<int, 4>{}, kt + 4);
+        step(std::integral_constant<int, 5>{}, kt + 5);
+        step(std::integral_constant<int, 6>{}, kt + 6);
+        step(std::integral_constant<int, 7>{}, kt + 7);
+    }
+    // Remainder: fewer than NS tiles, in stages 0, 1, ...
+    if (kt < g.nk) step(std::integral_constant<int, 0>{}, kt);
+    if (kt + 1 < g.nk) step(std::integral_constant<int, 1>{}, kt + 1);
+    if (kt + 2 < g.nk) step(std::integral_constant<int, 2>{}, kt + 2);
+    if (kt + 3 < g.nk) step(std::integral_constant<int, 3>{}, kt + 3);
+    if (kt + 4 < g.nk) step(std::integral_constant<int, 4>{}, kt + 4);
+    if (kt + 5 < g.nk) step(std::integral_constant<int, 5>{}, kt + 5);
+    if (kt + 6 < g.nk) step(std::integral_constant<int, 6>{}, kt + 6);
+    g.finish();   // the last tile's deferred MFMAs
+
+    auto stage_rt = [&](int b) -> _Float16* {
+        _Float16* p = st0;
+        if (b == 1) p = st1;
+        if constexpr (NS > 2) if (b == 2) p = st2;
+        if constexpr (NS > 3) if (b == 3) p = st3;
+        if constexpr (NS > 4) if (b == 4) p = st4;
+        if constexpr (NS > 5) if (b == 5) p = st5;
+        if constexpr (NS > 6) if (b == 6) p = st6;
+        if constexpr (NS > 7) if (b == 7) p = st7;
+        return p;
+    };
+    store_tile<BM, BN, NS, ACT, OUTT, NWV, LN, SZ>(g, stage_rt, sbias, R, C, M, N, ln);
 }
 
 template <int BM, int BN, int BK, int NS, int MODE, int ACT, int OUTT, int NWV = 4, int LN = -1>

@@ -61,7 +61,7 @@ EXPORTED_SYMBOLS = (
     "dotl_attention_split_plan", "dotl_wmma_set_split_kv", "dotl_wmma_split_kv_enabled",
     "dotl_wmma_set_split_count", "dotl_attention_forward_noalloc",
     "dotl_attention_noalloc_scratch_bytes", "dotl_linear_layernorm", "dotl_zero_rows",
-    "dotl_linear_planes",
+    "dotl_linear_planes", "dotl_ffn_layernorm",
 )
 
 _kernels = None
@@ -124,6 +124,9 @@ def _declare(lib) -> None:
     lib.dotl_linear_layernorm.restype = i32
     lib.dotl_linear_layernorm.argtypes = [vp, i32, vp, vp, vp, vp, vp, vp, c.c_double, vp, i32,
                                           vp, i64, vp, i64, i64, i64, i32, vp]
+    lib.dotl_ffn_layernorm.restype = i32
+    lib.dotl_ffn_layernorm.argtypes = [vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, c.c_double, vp,
+                                       i32, vp, i64, vp, i64, i64, i64, vp]
     lib.dotl_zero_rows.restype = i32
     lib.dotl_zero_rows.argtypes = [vp, vp, i64, i64, vp, vp]
     lib.dotl_attention_forward.restype = i32
@@ -575,6 +578,26 @@ class Kernels:
                 raise RuntimeError(f"{who}: residual must be float32 of shape {tuple(shape)}")
             rc_ = residual.contiguous()
         out = torch.empty(shape, dtype=torch.float32, device=xc.device) if store_out else None
+        nout, ncode, normed_rows, slot_ptr, orc = self._ln_outputs(
+            who, xc.device, shape, M, N, normed, out_row, normed_rows, io)
+        rc = self._check(self._lib.dotl_linear_layernorm(
+            xc.data_ptr(), DOTL_F16, hi.data_ptr(), bias.contiguous().data_ptr(),
+            rc_.data_ptr() if rc_ is not None else None,
+            out.data_ptr() if out is not None else None, ln_weight.contiguous().data_ptr(),
+            ln_bias.contiguous().data_ptr(), float(eps), nout.data_ptr(), ncode,
+            orc.data_ptr() if orc is not None else None, int(normed_rows), slot_ptr, M, N, K,
+            int(tile), self._stream(x.device)))
+        if rc == DOTL_DECLINED:
+            return None
+        return out, nout
+
+    @staticmethod
+    def _ln_outputs(who, device, shape, M, N, normed, out_row, normed_rows, io):
+        """The normed output of a LayerNorm epilogue (linear_layernorm,
+        ffn_layernorm) and its arguments: (tensor, dtype code, normed_rows,
+        graph I/O slot pointer or None, out_row contiguous or None)."""
+        import torch
+
         if out_row is not None:
             if out_row.dtype != torch.int32 or out_row.numel() != M or normed != "float":
                 raise RuntimeError(f"{who}: out_row must be int32 [{M}] with a float normed output")
@@ -585,13 +608,13 @@ class Kernels:
             normed_rows = M
             nshape = shape
         if normed == "split":
-            nout = torch.empty((2, *nshape), dtype=torch.float16, device=xc.device)
+            nout = torch.empty((2, *nshape), dtype=torch.float16, device=device)
             ncode = DOTL_F16X2
         elif normed == "half":
-            nout = torch.empty(nshape, dtype=torch.float16, device=xc.device)
+            nout = torch.empty(nshape, dtype=torch.float16, device=device)
             ncode = DOTL_F16
         elif normed == "float":
-            nout = torch.empty(nshape, dtype=torch.float32, device=xc.device)
+            nout = torch.empty(nshape, dtype=torch.float32, device=device)
             ncode = DOTL_F32
         else:
             raise RuntimeError(f"{who}: normed must be 'float', 'half' or 'split'")
@@ -602,13 +625,55 @@ class Kernels:
                 raise RuntimeError(f"{who}: io must be (a CUDA int64 slot of 2, 2)")
             slot_ptr = slot.data_ptr()
         orc = out_row.contiguous() if out_row is not None else None
-        rc = self._check(self._lib.dotl_linear_layernorm(
-            xc.data_ptr(), DOTL_F16, hi.data_ptr(), bias.contiguous().data_ptr(),
-            rc_.data_ptr() if rc_ is not None else None,
+        return nout, ncode, int(normed_rows), slot_ptr, orc
+
+    def ffn_layernorm(self, x, w1, b1, w2, b2, residual, ln_weight, ln_bias, eps=1e-5,
+                      normed="float", store_out=False, out_row=None, normed_rows=None, io=None):
+        """(y, LayerNorm(y)) with y = residual + GELU(x @ w1^T + b1) @ w2^T + b2
+        in one kernel, for d_model 256 and d_ff a multiple of 64 up to 2048.
+
+        Not in the reference's surface: linear_gelu(x, w1, b1, out_half=True)
+        followed by linear_layernorm(h, w2, b2, residual, ...), bit for bit.
+        `x` fp16 [..., 256]; w1 [d_ff, 256], w2 [256, d_ff] fp32 (their fp16
+        copies come from the weight cache); `residual` fp32 like y or None;
+        `normed`, `out_row`, `normed_rows` and `io` as in linear_layernorm;
+        y is returned only with store_out (else None). Returns None where the
+        kernel declines (the caller runs the two GEMMs)."""
+        import torch
+
+        who = "ffn_layernorm"
+        self._require_cuda(who, x, w1, b1, w2, b2, residual, ln_weight, ln_bias, out_row)
+        if (w1.dim() != 2 or w2.dim() != 2 or x.shape[-1] != w1.shape[1]
+                or tuple(w2.shape) != (w1.shape[1], w1.shape[0])):
+            raise RuntimeError(f"{who}: x [..., D], w1 [F, D] and w2 [D, F] required")
+        if (x.dtype != torch.float16 or w1.dtype != torch.float32 or w2.dtype != torch.float32
+                or b1.dtype != torch.float32 or b2.dtype != torch.float32):
+            return None
+        F, D = w1.shape
+        if (ln_weight.numel() != D or ln_bias.numel() != D or ln_weight.dtype != torch.float32
+                or ln_bias.dtype != torch.float32 or b1.numel() != F or b2.numel() != D):
+            raise RuntimeError(f"{who}: biases and LayerNorm weight/bias must be float32 of "
+                               f"{F} / {D} elements")
+        xc = x.contiguous()
+        M = xc.numel() // D
+        shape = (*xc.shape[:-1], D)
+        w1h, _ = self.weight_half(w1, False)
+        w2h, _ = self.weight_half(w2, False)
+        rc_ = None
+        if residual is not None:
+            if residual.dtype != torch.float32 or tuple(residual.shape) != tuple(shape):
+                raise RuntimeError(f"{who}: residual must be float32 of shape {tuple(shape)}")
+            rc_ = residual.contiguous()
+        out = torch.empty(shape, dtype=torch.float32, device=xc.device) if store_out else None
+        nout, ncode, normed_rows, slot_ptr, orc = self._ln_outputs(
+            who, xc.device, shape, M, D, normed, out_row, normed_rows, io)
+        rc = self._check(self._lib.dotl_ffn_layernorm(
+            xc.data_ptr(), DOTL_F16, w1h.data_ptr(), b1.contiguous().data_ptr(), w2h.data_ptr(),
+            b2.contiguous().data_ptr(), rc_.data_ptr() if rc_ is not None else None,
             out.data_ptr() if out is not None else None, ln_weight.contiguous().data_ptr(),
             ln_bias.contiguous().data_ptr(), float(eps), nout.data_ptr(), ncode,
-            orc.data_ptr() if orc is not None else None, int(normed_rows), slot_ptr, M, N, K,
-            int(tile), self._stream(x.device)))
+            orc.data_ptr() if orc is not None else None, normed_rows, slot_ptr, M, D, F,
+            self._stream(x.device)))
         if rc == DOTL_DECLINED:
             return None
         return out, nout

@@ -6,12 +6,13 @@ through the module (`config.CUDA_GRAPH = "off"`): a `from ... import` binds
 the value, not the setting. The thresholds below were re-derived for MI355X
 (256 CUs, 288 GB HBM3E) rather than carried over from the reference's card.
 
-Six knobs are new in this build:
+Seven knobs are new in this build:
   QKV_PRECISION  arithmetic of the fused QKV projection (auto, fp16x2, fp16x3, fp16)
   GELU_FP16      whether linear_gelu stores its output as fp16 for ffn_out
   ROW_PACKING    whether a padded batch runs on its valid rows only
   RESIDUAL_EPILOGUE  whether out_proj and ffn_out add the residual stream
   LN_EPILOGUE    whether they also apply the following LayerNorm (narrow rows)
+  FFN_LN         whether the whole FFN (+ residual, + LayerNorm) runs as one kernel
 """
 
 # Attention backend. One legal value: the custom kernels, never a prebuilt
@@ -176,6 +177,14 @@ _LN_EPILOGUE_MAX_D = 256
 # workgroup a CU) needs a few hundred tiles. Same-box A/B (layer µs, on /
 # off): C5 (85 104 rows) 518 / 530; C1 (128 rows, one tile) 54.6 / 35.4.
 _LN_EPILOGUE_MIN_ROWS = 32768
+
+# The FFN as one kernel (ffn_in, GELU, ffn_out, the residual add and the
+# following LayerNorm; dotl_ffn_layernorm): "auto" where the LayerNorm
+# epilogue above applies to ffn_out, d_model is 256 and d_ff a multiple of
+# 64 up to 2048 (C5). The hidden activations then stay in LDS, a step of 64
+# at a time, instead of making a round trip through HBM; outputs are
+# bit-identical to the two GEMMs. "off" runs the two GEMMs.
+FFN_LN = "auto"
 
 # Arithmetic of a model with more than one block. Each block's fp16 operand
 # roundings add to the residual stream the next block reads, so the error at

@@ -161,7 +161,7 @@ def _graph_key(x: torch.Tensor, use_mask: bool, packing=None) -> Tuple:
     and every knob that selects a kernel or an arithmetic."""
     return (tuple(x.shape), x.dtype, x.device.index, use_mask,
             None if packing is None else packing.key(), config.ROW_PACKING,
-            config.RESIDUAL_EPILOGUE, config.LN_EPILOGUE, config.ATTENTION_IMPL, config.LINEAR_GELU,
+            config.RESIDUAL_EPILOGUE, config.LN_EPILOGUE, config.FFN_LN, config.ATTENTION_IMPL, config.LINEAR_GELU,
             config.LINEAR_BIAS, config.LAYERNORM, config.QKV_FP16, config.NORMED_FP16,
             config.CP_ASYNC, config.ATTENTION_PRECISION, config.QKV_PRECISION, config.GELU_FP16,
             _kernels_mod._stack_precision, _kernels_mod._qkv_few_keys,

@@ -464,6 +464,29 @@ def _ln_epilogue_wanted(rows: int, width: int) -> bool:
             and rows >= config._LN_EPILOGUE_MIN_ROWS)
 
 
+def _ln_epilogue_call(call, width: int, kind: str, store_out: bool, packing, output: bool):
+    """Run a kernel with the LayerNorm epilogue (`call(**kw)`: linear_layernorm
+    or ffn_layernorm with every other argument bound) in the layer's form:
+    with `packing` its normed rows land in the padded [B, S, width] layout
+    (fp32) and the padded rows are zeroed; `output` binds the normed tensor
+    to a captured graph's output slot. None where the kernel declines."""
+    io = _output_io() if output else None
+    if packing is not None:
+        res = call(normed="float", store_out=store_out, out_row=packing.idx,
+                   normed_rows=packing.batch * packing.seq_len, io=io)
+        if res is None:
+            return None
+        h, out = res
+        _custom_kernels().zero_rows(out, packing.inv, io=io)
+        out = _note_output(out, io)
+        return h, out.view(packing.batch, packing.seq_len, width)
+    res = call(normed=kind, store_out=store_out, io=io)
+    if res is None:
+        return None
+    h, out = res
+    return h, _note_output(out, io)
+
+
 def _linear_norm(x: torch.Tensor, lin, residual: torch.Tensor, norm, kind: str,
                  store_out: bool = True, packing=None, output: bool = False):
     """(residual + lin(x), norm of that): `kind` is the normed form, "float",
@@ -482,30 +505,52 @@ def _linear_norm(x: torch.Tensor, lin, residual: torch.Tensor, norm, kind: str,
     if _ln_epilogue_wanted(rows, width) and x.dtype == torch.float16 and lin.bias is not None:
         kernels = _custom_kernels()
         if kernels is not None:
-            io = _output_io() if output else None
-            if packing is not None:
-                res = kernels.linear_layernorm(
-                    x, lin.weight, lin.bias, residual, norm.weight, norm.bias, norm.eps,
-                    normed="float", store_out=store_out, out_row=packing.idx,
-                    normed_rows=packing.batch * packing.seq_len, io=io)
-                if res is not None:
-                    h, out = res
-                    kernels.zero_rows(out, packing.inv, io=io)
-                    out = _note_output(out, io)
-                    return h, out.view(packing.batch, packing.seq_len, width)
-            else:
-                res = kernels.linear_layernorm(x, lin.weight, lin.bias, residual, norm.weight,
-                                               norm.bias, norm.eps, normed=kind,
-                                               store_out=store_out, io=io)
-                if res is not None:
-                    h, out = res
-                    return h, _note_output(out, io)
+            res = _ln_epilogue_call(
+                lambda **kw: kernels.linear_layernorm(x, lin.weight, lin.bias, residual,
+                                                      norm.weight, norm.bias, norm.eps, **kw),
+                width, kind, store_out, packing, output)
+            if res is not None:
+                return res
     h = _linear_bias(x, lin.weight, lin.bias, residual=residual)
     if packing is not None:
         return h, _layernorm_unpack(h, norm, packing)
     if kind == "split":
         return h, _layernorm_split(h, norm)
     return h, _layernorm(h, norm, out_half=kind == "half", output=output)
+
+
+def _ffn_ln_wanted(x: torch.Tensor, ffn_in, ffn_out) -> bool:
+    """Run the FFN, its residual add and the following LayerNorm as one
+    kernel (config.FFN_LN)? Exactly where the two GEMMs it replaces would be
+    the one-pass GELU GEMM with an fp16 output and the GEMM with the
+    LayerNorm epilogue, and the kernel's shapes hold."""
+    rows, d_model = x.numel() // x.shape[-1], x.shape[-1]
+    d_ff = ffn_in.weight.shape[0]
+    return (config.FFN_LN != "off" and x.dtype == torch.float16 and _lg() == "auto"
+            and ffn_in.bias is not None and ffn_out.bias is not None
+            and _gelu_output_wants_fp16(rows) and _ln_epilogue_wanted(rows, d_model)
+            and d_model == 256 and d_ff % 64 == 0 and d_ff <= 2048)
+
+
+def _ffn_norm(x: torch.Tensor, ffn_in, ffn_out, residual: torch.Tensor, norm, kind: str,
+              store_out: bool = True, packing=None, output: bool = False):
+    """(residual + ffn_out(GELU(ffn_in(x))), norm of that), the forms and
+    arguments as _linear_norm's: one kernel where _ffn_ln_wanted (the hidden
+    activations never reach memory; bit-identical to the two GEMMs), else
+    _linear_gelu followed by _linear_norm."""
+    rows = x.numel() // x.shape[-1]
+    if _ffn_ln_wanted(x, ffn_in, ffn_out):
+        kernels = _custom_kernels()
+        if kernels is not None:
+            res = _ln_epilogue_call(
+                lambda **kw: kernels.ffn_layernorm(x, ffn_in.weight, ffn_in.bias, ffn_out.weight,
+                                                   ffn_out.bias, residual, norm.weight,
+                                                   norm.bias, norm.eps, **kw),
+                x.shape[-1], kind, store_out, packing, output)
+            if res is not None:
+                return res
+    hidden = _linear_gelu(x, ffn_in, out_half=_gelu_output_wants_fp16(rows))
+    return _linear_norm(hidden, ffn_out, residual, norm, kind, store_out, packing, output)
 
 
 def _ffn_block_eligible(x, ffn_in, ffn_out) -> bool:

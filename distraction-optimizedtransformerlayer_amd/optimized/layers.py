@@ -20,7 +20,7 @@ from .kernels import (_add_layernorm, _add_layernorm_output, _add_layernorm_spli
                       _ffn_block, _ffn_block_eligible, _gelu_input_wants_fp16,
                       _gelu_output_wants_fp16, _layernorm, _layernorm_split,
                       _linear_bias, _linear_bias_split, _linear_bias_split_prefix,
-                      _linear_gelu, _linear_norm,
+                      _ffn_norm, _linear_gelu, _linear_norm,
                       _normed_split_wanted, _normed_wants_fp16, _qkv_math_code,
                       _residual_epilogue_wanted)
 from .util import _version_or_none
@@ -257,24 +257,24 @@ class MyTransformerBlock(nn.Module):
         formed in the GEMM epilogues (the same fp32 sums the add+LayerNorm
         kernels would form), each followed by its LayerNorm -- in the same
         epilogue where the rows are narrow enough (_linear_norm), else as a
-        plain LayerNorm of h1 / h2. Outputs are bit-identical to the
-        add+LayerNorm chain."""
+        plain LayerNorm of h1 / h2; at d_model 256 the whole FFN with its add
+        and LayerNorm is one kernel (_ffn_norm). Outputs are bit-identical to
+        the add+LayerNorm chain."""
         rows = x.numel() // x.shape[-1]
         width = x.shape[-1]
         kind2 = "half" if _gelu_input_wants_fp16(rows, width) else "float"
         h1, normed2 = self.attention(normed, None, self.causal, True, packing=packing, residual=x,
                                      norm=self.norm2, norm_kind=kind2)
-        hidden = _linear_gelu(normed2, self.ffn_in, out_half=_gelu_output_wants_fp16(rows))
         if next_norm_is_output:
             # the model's output: never narrowed; the sum is not read after it
-            h2, out = _linear_norm(hidden, self.ffn_out, h1, next_norm, "float", store_out=False,
-                                   packing=packing, output=True)
+            h2, out = _ffn_norm(normed2, self.ffn_in, self.ffn_out, h1, next_norm, "float",
+                                store_out=False, packing=packing, output=True)
             return (None if packing is not None else h2), out
         if _normed_split_wanted():
             kind = "split"
         else:
             kind = "half" if _normed_wants_fp16(rows, width) else "float"
-        return _linear_norm(hidden, self.ffn_out, h1, next_norm, kind)
+        return _ffn_norm(normed2, self.ffn_in, self.ffn_out, h1, next_norm, kind)
 
     def _forward_packed(self, x, normed, next_norm, next_norm_is_output, packing):
         if self._residual_fused(x):

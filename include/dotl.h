@@ -254,6 +254,32 @@ int dotl_linear_layernorm(const void* x, int x_dtype, const void* w_hi, const fl
                           int64_t M, int64_t N, int64_t K, int tile, void* stream);
 
 /*
+ * The position-wise FFN with the residual add and the row LayerNorm in one
+ * kernel, for d_model 256:
+ *   h = GELU(x W1^T + b1) in fp16, y = residual + h W2^T + b2,
+ *   normed = LayerNorm(y) * ln_weight + ln_bias.
+ * Replaces linear_gelu, then linear_bias and fused_add_layernorm
+ * (csrc/linear_gelu.cuh:598-756, csrc/add_layernorm.cuh:491-692, as
+ * optimized/layers.py chains them); equals dotl_linear (GELU, fp16 out)
+ * followed by dotl_linear_layernorm bit for bit, without writing h to
+ * memory. No counterpart entry in the reference.
+ *   x            fp16 [M, D], D == 256
+ *   w1_hi        fp16 [F, D], w2_hi fp16 [D, F] (dotl_weight_split);
+ *                F a positive multiple of 64 up to 2048
+ *   b1           fp32 [F]; b2 fp32 [D]
+ *   residual     optional (NULL) fp32 [M, D]
+ *   out          optional (NULL: y is not stored) fp32 [M, D]
+ *   normed, normed_dtype, out_row, normed_rows, io: as dotl_linear_layernorm
+ * Declines (DOTL_DECLINED) for other shapes and operand types: the caller
+ * runs the two GEMMs. Every tensor 16-byte aligned.
+ */
+int dotl_ffn_layernorm(const void* x, int x_dtype, const void* w1_hi, const float* b1,
+                       const void* w2_hi, const float* b2, const float* residual, float* out,
+                       const float* ln_weight, const float* ln_bias, double eps, void* normed,
+                       int normed_dtype, const int32_t* out_row, int64_t normed_rows,
+                       const int64_t* io, int64_t M, int64_t D, int64_t F, void* stream);
+
+/*
  * Zero row r of out (fp32 [rows, width]) wherever row_map[r] < 0: the padded
  * rows of a padded batch's output, whose valid rows dotl_linear_layernorm
  * scattered there (row_map is the padded -> packed map, -1 for padding; the

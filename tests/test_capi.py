@@ -242,6 +242,32 @@ def test_linear_planes_checks(lib):
     assert f(None, None, None, None, None, None, 0, 0, 64, 64, 2, -1, None) == 0
 
 
+def test_ffn_layernorm_checks(lib):
+    """The fused FFN: argument errors, then declines (1) for what the kernel
+    does not serve, before any device work."""
+    f = lib.dotl_ffn_layernorm
+    n = None
+
+    def call(x_dtype=1, normed_dtype=0, out_row=None, normed_rows=4, M=4, D=256, F=1024):
+        return f(n, x_dtype, n, n, n, n, n, n, n, n, 1e-5, n, normed_dtype, out_row, normed_rows,
+                 n, M, D, F, n)
+
+    assert call(normed_dtype=3) == -1
+    assert b"normed output" in lib.dotl_last_error()
+    row = ctypes.c_void_p(16)    # never dereferenced: every call below fails its checks first
+    assert call(normed_dtype=1, out_row=row, normed_rows=8) == -1
+    assert b"out_row" in lib.dotl_last_error()
+    assert call(normed_rows=5) == -1
+    assert b"rows" in lib.dotl_last_error()
+    assert call(M=-1) == -1
+    # declines: fp32 x, d_model other than 256, d_ff not a multiple of 64 or above 2048
+    for kw in ({"x_dtype": 0}, {"D": 128}, {"F": 96}, {"F": 4096}, {"F": 0}):
+        assert call(**kw) == 1, kw
+    assert call(M=0, normed_rows=0) == 0
+    assert call() == -1
+    assert b"null pointer" in lib.dotl_last_error()
+
+
 def test_zero_rows_checks(lib):
     assert lib.dotl_zero_rows(None, None, 4, 8, None, None) == -1
     assert b"null pointer" in lib.dotl_last_error()
