@@ -302,12 +302,10 @@ def layer_ops(cfg, model, x, mask):
             # kernel (optimized.kernels._ffn_norm)
             def ffn_fused():
                 if packing is not None:
-                    _, out = kx.ffn_layernorm(n2, layer.ffn_in.weight, layer.ffn_in.bias,
-                                              layer.ffn_out.weight, layer.ffn_out.bias, h1, fw,
-                                              fb, 1e-5, "float", out_row=packing.idx,
-                                              normed_rows=T)
-                    kx.zero_rows(out, packing.inv)
-                    return out
+                    return kx.ffn_layernorm(n2, layer.ffn_in.weight, layer.ffn_in.bias,
+                                            layer.ffn_out.weight, layer.ffn_out.bias, h1, fw, fb,
+                                            1e-5, "float", out_row=packing.idx, normed_rows=T,
+                                            zero_padded=True)[1]
                 return kx.ffn_layernorm(n2, layer.ffn_in.weight, layer.ffn_in.bias,
                                         layer.ffn_out.weight, layer.ffn_out.bias, h1, fw, fb,
                                         1e-5, "float")[1]

@@ -44,7 +44,7 @@ __global__ __launch_bounds__(kWaves * 64) void ffn_ln_kernel(
     const _Float16* __restrict__ X, const _Float16* __restrict__ W1,
     const float* __restrict__ b1, const _Float16* __restrict__ W2,
     const float* __restrict__ b2, const float* __restrict__ R, void* __restrict__ C, int64_t M,
-    int64_t F, LnEpi ln) {
+    int64_t F, LnEpi ln, int zero_padded) {
     // The second product is the 128x256 tile of the GEMM (8 waves, 2 x 4,
     // each a 64 x 64 block): its fragment reader, MFMA and accumulators.
     using G = DmaGemm<kBM, kD, 64, 2, 0, DOTL_ACT_NONE, DOTL_F32, kWaves>;
@@ -112,6 +112,44 @@ __global__ __launch_bounds__(kWaves * 64) void ffn_ln_kernel(
             dma16_off(W1 + c * kFC * kD, off1[rd], stage + (kW1Row + rd * 64 + g.wave * 8) * 64);
     };
 
+    // zero_padded: the rows of the (fp32) normed output that out_row skips
+    // -- those after each of this workgroup's rows up to the next named one,
+    // and, in workgroup 0, those before the first -- written with zeros, one
+    // 1 KiB row a wave instruction, during the first step: the stores then
+    // drain under its products (the next step's wait covers them), where at
+    // the end of the launch they measured as slow as a separate pass. The
+    // rows are disjoint from every named row. Lane u holds out_row of this
+    // wave's u-th row (u <= 16; loaded before the first DMA, so its wait
+    // does not take the DMAs with it).
+    const bool zeroing = zero_padded && ln.out_row != nullptr;
+    constexpr int kRowsPerWave = kBM / kWaves;
+    const int64_t zlo = g.m0 + kRowsPerWave * g.wave;
+    int zr = 0;
+    if (zeroing && g.lane <= kRowsPerWave) {
+        const int64_t m = zlo + g.lane;
+        zr = ln.out_row[m < M ? m : M - 1];
+    }
+    auto zero_padded_rows = [&]() {
+        float* nout = static_cast<float*>(ln.io != nullptr ? reinterpret_cast<void*>(ln.io[1])
+                                                           : ln.normed);
+        const int64_t rows = ln.plane / kD;
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        auto zero = [&](int64_t lo, int64_t hi) {
+            hi = hi < rows ? hi : rows;
+            for (int64_t r = lo; r < hi; ++r)
+                *reinterpret_cast<float4*>(nout + r * kD + 4 * g.lane) = z;
+        };
+        static_for<0, kRowsPerWave>([&](auto uu) {
+            constexpr int u = decltype(uu)::value;
+            const int64_t m = zlo + u;
+            if (m < M) {
+                const int64_t next = m + 1 < M ? __builtin_amdgcn_readlane(zr, u + 1) : rows;
+                zero(static_cast<int64_t>(__builtin_amdgcn_readlane(zr, u)) + 1, next);
+            }
+        });
+        if (blockIdx.x == 0 && g.wave == 0) zero(0, __builtin_amdgcn_readlane(zr, 0));
+    };
+
     const int tr = 32 * hr + g.lr;   // this lane's h row (tile-local)
     auto step = [&](auto sc, int64_t c) {
         constexpr int S = decltype(sc)::value;
@@ -121,6 +159,7 @@ __global__ __launch_bounds__(kWaves * 64) void ffn_ln_kernel(
         // done with step c - 1 (h block and the other stage free)
         wait_vmcnt<0>();
         stage_barrier();
+        if (c == 0 && zeroing) zero_padded_rows();
         if (c + 1 < g.nk) issue(nxt, c + 1);
         // h block: 16 MFMAs over d_model, k in order (the GEMM's sequence)
         floatx16 h = floatx16{};
@@ -178,9 +217,10 @@ __global__ __launch_bounds__(kWaves * 64) void ffn_ln_kernel(
 template <int LN>
 void launch(const _Float16* X, const _Float16* W1, const float* b1, const _Float16* W2,
             const float* b2, const float* R, void* C, int64_t M, int64_t F, const LnEpi& ln,
-            hipStream_t stream) {
+            int zero_padded, hipStream_t stream) {
     hipLaunchKernelGGL((ffn_ln_kernel<LN>), dim3(static_cast<unsigned>((M + kBM - 1) / kBM)),
-                       dim3(kWaves * 64), 0, stream, X, W1, b1, W2, b2, R, C, M, F, ln);
+                       dim3(kWaves * 64), 0, stream, X, W1, b1, W2, b2, R, C, M, F, ln,
+                       zero_padded);
 }
 
 }  // namespace
@@ -192,8 +232,8 @@ extern "C" int dotl_ffn_layernorm(const void* x, int x_dtype, const void* w1_hi,
                                   float* out, const float* ln_weight, const float* ln_bias,
                                   double eps, void* normed, int normed_dtype,
                                   const int32_t* out_row, int64_t normed_rows,
-                                  const int64_t* io, int64_t M, int64_t D, int64_t F,
-                                  void* stream) {
+                                  int zero_padded, const int64_t* io, int64_t M, int64_t D,
+                                  int64_t F, void* stream) {
     using namespace dotl;
     using namespace dotl::gemm_dma;
     clear_error();
@@ -207,6 +247,8 @@ extern "C" int dotl_ffn_layernorm(const void* x, int x_dtype, const void* w1_hi,
                  static_cast<long long>(M));
     DOTL_REQUIRE(out_row == nullptr || normed_dtype == DOTL_F32,
                  "%s: scattered rows (out_row) take a float32 normed output", who);
+    DOTL_REQUIRE(zero_padded == 0 || out_row != nullptr,
+                 "%s: zero_padded applies to scattered rows (out_row)", who);
     if (x_dtype != DOTL_F16 || D != kD || F % kFC != 0 || F == 0 || F > kMaxF ||
         M * D * 2 >= (int64_t{1} << 32)) {
         set_error(std::string(who) + ": served for a float16 x, d_model 256 and d_ff a positive "
@@ -233,16 +275,16 @@ extern "C" int dotl_ffn_layernorm(const void* x, int x_dtype, const void* w1_hi,
     const bool wc = out != nullptr;
     switch (normed_dtype) {
         case DOTL_F32:
-            wc ? launch<DOTL_F32 + 4>(xh, w1, b1, w2, b2, residual, out, M, F, ln, s)
-               : launch<DOTL_F32>(xh, w1, b1, w2, b2, residual, out, M, F, ln, s);
+            wc ? launch<DOTL_F32 + 4>(xh, w1, b1, w2, b2, residual, out, M, F, ln, zero_padded, s)
+               : launch<DOTL_F32>(xh, w1, b1, w2, b2, residual, out, M, F, ln, zero_padded, s);
             break;
         case DOTL_F16:
-            wc ? launch<DOTL_F16 + 4>(xh, w1, b1, w2, b2, residual, out, M, F, ln, s)
-               : launch<DOTL_F16>(xh, w1, b1, w2, b2, residual, out, M, F, ln, s);
+            wc ? launch<DOTL_F16 + 4>(xh, w1, b1, w2, b2, residual, out, M, F, ln, zero_padded, s)
+               : launch<DOTL_F16>(xh, w1, b1, w2, b2, residual, out, M, F, ln, zero_padded, s);
             break;
         default:
-            wc ? launch<DOTL_F16X2 + 4>(xh, w1, b1, w2, b2, residual, out, M, F, ln, s)
-               : launch<DOTL_F16X2>(xh, w1, b1, w2, b2, residual, out, M, F, ln, s);
+            wc ? launch<DOTL_F16X2 + 4>(xh, w1, b1, w2, b2, residual, out, M, F, ln, zero_padded, s)
+               : launch<DOTL_F16X2>(xh, w1, b1, w2, b2, residual, out, M, F, ln, zero_padded, s);
             break;
     }
     return check_launch(who);

@@ -126,7 +126,7 @@ def _declare(lib) -> None:
                                           vp, i64, vp, i64, i64, i64, i32, vp]
     lib.dotl_ffn_layernorm.restype = i32
     lib.dotl_ffn_layernorm.argtypes = [vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, c.c_double, vp,
-                                       i32, vp, i64, vp, i64, i64, i64, vp]
+                                       i32, vp, i64, i32, vp, i64, i64, i64, vp]
     lib.dotl_zero_rows.restype = i32
     lib.dotl_zero_rows.argtypes = [vp, vp, i64, i64, vp, vp]
     lib.dotl_attention_forward.restype = i32
@@ -628,7 +628,8 @@ class Kernels:
         return nout, ncode, int(normed_rows), slot_ptr, orc
 
     def ffn_layernorm(self, x, w1, b1, w2, b2, residual, ln_weight, ln_bias, eps=1e-5,
-                      normed="float", store_out=False, out_row=None, normed_rows=None, io=None):
+                      normed="float", store_out=False, out_row=None, normed_rows=None, io=None,
+                      zero_padded=False):
         """(y, LayerNorm(y)) with y = residual + GELU(x @ w1^T + b1) @ w2^T + b2
         in one kernel, for d_model 256 and d_ff a multiple of 64 up to 2048.
 
@@ -637,8 +638,10 @@ class Kernels:
         `x` fp16 [..., 256]; w1 [d_ff, 256], w2 [256, d_ff] fp32 (their fp16
         copies come from the weight cache); `residual` fp32 like y or None;
         `normed`, `out_row`, `normed_rows` and `io` as in linear_layernorm;
-        y is returned only with store_out (else None). Returns None where the
-        kernel declines (the caller runs the two GEMMs)."""
+        `zero_padded` (with an increasing out_row): the rows out_row does not
+        name are zeroed too (no zero_rows call needed). y is returned only
+        with store_out (else None). Returns None where the kernel declines
+        (the caller runs the two GEMMs)."""
         import torch
 
         who = "ffn_layernorm"
@@ -672,7 +675,8 @@ class Kernels:
             b2.contiguous().data_ptr(), rc_.data_ptr() if rc_ is not None else None,
             out.data_ptr() if out is not None else None, ln_weight.contiguous().data_ptr(),
             ln_bias.contiguous().data_ptr(), float(eps), nout.data_ptr(), ncode,
-            orc.data_ptr() if orc is not None else None, normed_rows, slot_ptr, M, D, F,
+            orc.data_ptr() if orc is not None else None, normed_rows,
+            1 if (zero_padded and orc is not None) else 0, slot_ptr, M, D, F,
             self._stream(x.device)))
         if rc == DOTL_DECLINED:
             return None

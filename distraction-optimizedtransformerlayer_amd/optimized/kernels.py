@@ -464,20 +464,24 @@ def _ln_epilogue_wanted(rows: int, width: int) -> bool:
             and rows >= config._LN_EPILOGUE_MIN_ROWS)
 
 
-def _ln_epilogue_call(call, width: int, kind: str, store_out: bool, packing, output: bool):
+def _ln_epilogue_call(call, width: int, kind: str, store_out: bool, packing, output: bool,
+                      zeroes_padded: bool = False):
     """Run a kernel with the LayerNorm epilogue (`call(**kw)`: linear_layernorm
     or ffn_layernorm with every other argument bound) in the layer's form:
     with `packing` its normed rows land in the padded [B, S, width] layout
-    (fp32) and the padded rows are zeroed; `output` binds the normed tensor
-    to a captured graph's output slot. None where the kernel declines."""
+    (fp32) and the padded rows are zeroed (by the kernel itself where
+    `zeroes_padded`, else by zero_rows); `output` binds the normed tensor to
+    a captured graph's output slot. None where the kernel declines."""
     io = _output_io() if output else None
     if packing is not None:
+        extra = {"zero_padded": True} if zeroes_padded else {}
         res = call(normed="float", store_out=store_out, out_row=packing.idx,
-                   normed_rows=packing.batch * packing.seq_len, io=io)
+                   normed_rows=packing.batch * packing.seq_len, io=io, **extra)
         if res is None:
             return None
         h, out = res
-        _custom_kernels().zero_rows(out, packing.inv, io=io)
+        if not zeroes_padded:
+            _custom_kernels().zero_rows(out, packing.inv, io=io)
         out = _note_output(out, io)
         return h, out.view(packing.batch, packing.seq_len, width)
     res = call(normed=kind, store_out=store_out, io=io)
@@ -546,7 +550,7 @@ def _ffn_norm(x: torch.Tensor, ffn_in, ffn_out, residual: torch.Tensor, norm, ki
                 lambda **kw: kernels.ffn_layernorm(x, ffn_in.weight, ffn_in.bias, ffn_out.weight,
                                                    ffn_out.bias, residual, norm.weight,
                                                    norm.bias, norm.eps, **kw),
-                x.shape[-1], kind, store_out, packing, output)
+                x.shape[-1], kind, store_out, packing, output, zeroes_padded=True)
             if res is not None:
                 return res
     hidden = _linear_gelu(x, ffn_in, out_half=_gelu_output_wants_fp16(rows))

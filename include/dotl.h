@@ -270,6 +270,9 @@ int dotl_linear_layernorm(const void* x, int x_dtype, const void* w_hi, const fl
  *   residual     optional (NULL) fp32 [M, D]
  *   out          optional (NULL: y is not stored) fp32 [M, D]
  *   normed, normed_dtype, out_row, normed_rows, io: as dotl_linear_layernorm
+ *   zero_padded  with out_row (strictly increasing): the rows of normed that
+ *                out_row does not name are written with zeros too (what
+ *                dotl_zero_rows would do after it); 0 leaves them untouched
  * Declines (DOTL_DECLINED) for other shapes and operand types: the caller
  * runs the two GEMMs. Every tensor 16-byte aligned.
  */
@@ -277,7 +280,8 @@ int dotl_ffn_layernorm(const void* x, int x_dtype, const void* w1_hi, const floa
                        const void* w2_hi, const float* b2, const float* residual, float* out,
                        const float* ln_weight, const float* ln_bias, double eps, void* normed,
                        int normed_dtype, const int32_t* out_row, int64_t normed_rows,
-                       const int64_t* io, int64_t M, int64_t D, int64_t F, void* stream);
+                       int zero_padded, const int64_t* io, int64_t M, int64_t D, int64_t F,
+                       void* stream);
 
 /*
  * Zero row r of out (fp32 [rows, width]) wherever row_map[r] < 0: the padded

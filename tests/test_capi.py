@@ -248,9 +248,10 @@ def test_ffn_layernorm_checks(lib):
     f = lib.dotl_ffn_layernorm
     n = None
 
-    def call(x_dtype=1, normed_dtype=0, out_row=None, normed_rows=4, M=4, D=256, F=1024):
+    def call(x_dtype=1, normed_dtype=0, out_row=None, normed_rows=4, M=4, D=256, F=1024,
+             zero_padded=0):
         return f(n, x_dtype, n, n, n, n, n, n, n, n, 1e-5, n, normed_dtype, out_row, normed_rows,
-                 n, M, D, F, n)
+                 zero_padded, n, M, D, F, n)
 
     assert call(normed_dtype=3) == -1
     assert b"normed output" in lib.dotl_last_error()
@@ -259,6 +260,8 @@ def test_ffn_layernorm_checks(lib):
     assert b"out_row" in lib.dotl_last_error()
     assert call(normed_rows=5) == -1
     assert b"rows" in lib.dotl_last_error()
+    assert call(zero_padded=1) == -1
+    assert b"zero_padded" in lib.dotl_last_error()
     assert call(M=-1) == -1
     # declines: fp32 x, d_model other than 256, d_ff not a multiple of 64 or above 2048
     for kw in ({"x_dtype": 0}, {"D": 128}, {"F": 96}, {"F": 4096}, {"F": 0}):

@@ -85,6 +85,22 @@ def test_ffn_ln_scatter_and_zero_rows(kernels, M, F, rows):
     kernels.zero_rows(n, inv)
     assert y is None
     assert torch.equal(n, n_ref)
+    # the kernel's own zeroing of the rows out_row skips (before the first,
+    # between, after the last) equals zero_rows'
+    for first in (0, 3):
+        orow = out_row if first == 0 else out_row + first - int(out_row[0].item())
+        if int(orow[-1].item()) >= rows:
+            continue
+        inv2 = torch.full((rows,), -1, dtype=torch.int32, device=DEV)
+        inv2[orow.long()] = torch.arange(M, dtype=torch.int32, device=DEV)
+        _, n_ref2 = kernels.linear_layernorm(h, w2, b2, r, lw, lb, EPS, store_out=False,
+                                             out_row=orow, normed_rows=rows)
+        kernels.zero_rows(n_ref2, inv2)
+        poison = torch.full((rows, D), float("nan"), device=DEV)
+        del poison
+        _, n2 = kernels.ffn_layernorm(x, w1, b1, w2, b2, r, lw, lb, EPS, out_row=orow,
+                                      normed_rows=rows, zero_padded=True)
+        assert torch.equal(n2, n_ref2)
 
 
 def test_ffn_ln_declines(kernels):
