@@ -386,7 +386,8 @@ def kernel_table(cfg, model, x, mask, reps):
 # Kernel-symbol substring of each op family (the --pmc CSV names dispatches
 # by symbol), and the calibration copy: dotl_smoke_test_identity over
 # COPY_FLOATS floats reads and writes exactly 4 * COPY_FLOATS bytes.
-KERNEL_FAMILY = (("attention", "attn_"), ("linear", "gemm"), ("layernorm", "layernorm"))
+KERNEL_FAMILY = (("ffn (", "ffn_ln_kernel"), ("attention", "attn_"), ("linear", "gemm"),
+                 ("layernorm", "layernorm"))
 COPY_SYMBOL = "identity_kernel"
 COPY_FLOATS = 64 << 20
 PROFILE_REPS = 5
