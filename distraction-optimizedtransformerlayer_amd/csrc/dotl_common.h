@@ -170,9 +170,17 @@ __device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
 // coefficients (a power of two: the Horner steps round exactly as before,
 // scaled). |x| is clamped at 2^64 in that product so that x = +-inf, where
 // q = 0, gives inf and 0 rather than 0 * inf. One reciprocal, one exp2 and
-// nine other operations; the device library's erff costs several times that,
-// and an epilogue that applies it to every output of a GEMM with a short K
-// spends more time there than in the MFMAs.
+// nine other operations; the device library's erff costs several times
+// that, and an epilogue that applies it to every output of a GEMM with a
+// short K spends more time there than in the MFMAs.
+// The fp32 result is fenced before any narrowing (see opaque), so an fp16
+// output is that value rounded, in every kernel. VOL picks the fence: a
+// volatile asm, which also bounds the compiler's scheduling regions, or a
+// plain one; the bits are the same. Measured on MI355X, the volatile one
+// schedules faster in the 8-wave GEMM tiles and the fused FFN kernel (C5
+// FFN 160 vs 170 us), the plain one in the 4-wave tiles (C2 ffn_in 15.5 vs
+// 17.5 us).
+template <bool VOL>
 __device__ __forceinline__ float gelu_erf(float x) {
     const float ax = fabsf(x);
     const float z = ax * 0.70710678118654752440f;
@@ -184,9 +192,12 @@ __device__ __forceinline__ float gelu_erf(float x) {
     poly *= t;
     // exp(-z^2) = exp2(-x^2 log2(e) / 2)
     const float hq = poly * __builtin_amdgcn_exp2f(x * (x * -0.72134752044448170368f));
-    // opaque: an fp16 output is this fp32 value narrowed, in every kernel
     float g = fmaf(hq, fminf(ax, 0x1p64f), fmaxf(x, 0.f));
-    opaque(g);
+    if constexpr (VOL) {
+        opaque(g);
+    } else {
+        asm("" : "+v"(g));
+    }
     return g;
 }
 

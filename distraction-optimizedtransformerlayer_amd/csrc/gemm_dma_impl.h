@@ -388,7 +388,7 @@ __device__ __forceinline__ void store_tile(G& g, BufFn stage_buf, const float* s
                             float a = g.acc[i][j][4 * grp + e];
                             if constexpr (G::SPLIT) a += g.acc2[i][j][4 * grp + e] * kLoUnscale;
                             a += sbias[cl + e];
-                            if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
+                            if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf<NWV == 8>(a);
                             v[e] = a;
                         }
                         TO* crow = static_cast<TO*>(C) + row * N;
@@ -548,7 +548,7 @@ __device__ __forceinline__ void store_tile(G& g, BufFn stage_buf, const float* s
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float a = v[e] + sbias[cl + e];
-                    if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf(a);
+                    if constexpr (ACT == DOTL_ACT_GELU) a = gelu_erf<NWV == 8>(a);
                     v[e] = a;
                 }
                 if constexpr (OUTT == DOTL_F32) {
