@@ -473,7 +473,7 @@ int linear_impl(const void* x, int x_dtype, const void* w_hi, const void* w_lo,
     DOTL_REQUIRE(math != DOTL_MATH_FP16X3 || w_lo != nullptr,
                  "%s: the fp16x3 math needs the split weight residual", who);
     DOTL_REQUIRE(((M + 63) / 64) * ((N + 63) / 64) <= 0x7fffffff, "%s: too large", who);
-    DOTL_REQUIRE(tile == -1 || (tile >= 0 && tile <= 18) || (tile >= 100 && tile <= 104),
+    DOTL_REQUIRE(tile == -1 || (tile >= 0 && tile <= 19) || (tile >= 100 && tile <= 104),
                  "%s: unknown tile id %d", who, tile);
     if (M == 0 || N == 0) return DOTL_OK;
     DOTL_REQUIRE(x && w_hi && bias && out, "%s: null pointer", who);

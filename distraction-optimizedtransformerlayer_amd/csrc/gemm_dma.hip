@@ -18,8 +18,10 @@ using gemm_dma::dispatch_tile;
 //   * split passes: two passes at K <= 512 on the 192x128 tile (C2's QKV,
 //     M = 3487: 228 tiles in one wave instead of a short second wave of
 //     128-row tiles, 20.5 vs 23.8 us; C5's: 125.8 vs 130.9 us; at K = 1024
-//     and 2048 it loses); else the 128x128 tile with 128-byte K rows when it
-//     fills the CUs, else the shallow 128x64, then 64x64.
+//     and 2048 it loses), with 8 waves (tile 19, two a SIMD: C5's QKV 100
+//     vs 110 us for the 4-wave tile 14, C2's 16.6 vs 18.0); else the 128x128
+//     tile with 128-byte K rows when it fills the CUs, else the shallow
+//     128x64, then 64x64.
 int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     if (passes == 1) {
@@ -43,7 +45,7 @@ int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
         if (tiles(128, 64) >= 200) return 13;
         return 8;
     }
-    if (passes == 2 && K <= 512 && tiles(192, 128) >= 200) return 14;
+    if (passes == 2 && K <= 512 && tiles(192, 128) >= 200) return 19;
     if (tiles(128, 128) >= 400) return 10;
     if (tiles(128, 64) >= 240) return 7;
     return 8;

@@ -887,6 +887,9 @@ bool dispatch_tile(const DmaArgs& a, int tile) {
         case 18:  // 128x256, 128-byte K rows, 3 stages of 48 KiB
             if constexpr (PASSES == 1) { launch_dma<128, 256, 64, 3, MODE, ACT, OUTT, 8>(a); return true; }
             return false;
+        case 19:  // 192x128 with 8 waves (each 96x32), split x: 2 stages of 64 KiB
+            if constexpr (PASSES == 2) { launch_dma<192, 128, 64, 2, MODE, ACT, OUTT, 8>(a); return true; }
+            return false;
     }
     return false;
 }

@@ -182,8 +182,9 @@ int dotl_weight_split(const float* w, void* w_hi, void* w_lo, int64_t n, void* s
  *             128-byte K rows; 14: 192x128 with 128-byte K rows [one or two
  *             passes]; 15-17: 8 waves a workgroup, two per SIMD, [one pass]:
  *             256x256 with 128-byte K rows, 256x256 with 64-byte K rows,
- *             256x128 with 128-byte K rows); 100 + id (id <= 4) forces the
- *             register-staged kernel (for measurement)
+ *             256x128 with 128-byte K rows; 18: 128x256, 8 waves [one pass];
+ *             19: 192x128, 8 waves [two passes]); 100 + id (id <= 4) forces
+ *             the register-staged kernel (for measurement)
  *   fp16 / split-fp16 x with K % 64 == 0 runs the LDS-DMA pipelined kernel;
  *   anything else the register-staged one. Declines when K % 8 != 0, or a
  *   DOTL_F16X2 x with K % 64 != 0.

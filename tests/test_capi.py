@@ -66,7 +66,7 @@ def test_linear_rejects_bad_codes(lib):
     assert lib.dotl_linear_residual(None, 1, None, None, None, None, None, 4, 4, 64, 0, 0, -1,
                                     None) == -1
     # tile ids beyond the menu
-    assert lib.dotl_linear(None, 1, None, None, None, None, 0, 4, 4, 64, 0, 0, 19, None) == -1
+    assert lib.dotl_linear(None, 1, None, None, None, None, 0, 4, 4, 64, 0, 0, 20, None) == -1
     assert b"unknown tile id" in lib.dotl_last_error()
     # empty problems launch nothing and succeed
     assert lib.dotl_linear(None, 0, None, None, None, None, 0, 0, 4, 16, 0, 0, -1, None) == 0

@@ -403,7 +403,7 @@ DMA_SHAPES = [(300, 200, 128), (1000, 1024, 256), (64, 2048, 512), (513, 384, 64
 
 ALL_TILES = [-1] + list(range(18))
 SPLIT_TILES = [-1, 0, 2, 4, 5, 7, 8, 10, 13]   # the tiles built for split passes
-TWO_PASS_TILES = SPLIT_TILES + [14]            # 192x128: one or two passes, not three
+TWO_PASS_TILES = SPLIT_TILES + [14, 19]        # 192x128 (4 / 8 waves): two passes at most
 
 
 @pytest.mark.parametrize("M,N,K", DMA_SHAPES)
