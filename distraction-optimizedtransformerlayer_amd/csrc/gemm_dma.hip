@@ -38,6 +38,10 @@ int pick_dma_tile(int64_t M, int64_t N, int64_t K, int passes) {
             return fill(tiles(256, 128)) > fill(tiles(256, 256)) + 0.1 ? 17 : 15;
         }
         if (tiles(128, 128) >= 960) return 12;
+        // a deep K on about one 128x128 tile a CU: the four-stage 128x128
+        // tile (C3's ffn_out, K = 4096: 41.2 vs 43.2 us for the 128x64 tile
+        // 13; an 8-wave two-stage 128x128 tile measured 46.5)
+        if (tiles(128, 128) >= 240 && K >= 4096) return 10;
         // about one 128x128 tile a CU at K = 1024: the three-stage 128x64
         // tile's twice as many workgroups (C3's out_proj, 15.7 vs 18.4 us)
         if (tiles(128, 128) < 320 && tiles(128, 64) >= 480 && K >= 1024) return 13;
