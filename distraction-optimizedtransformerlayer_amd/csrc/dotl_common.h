@@ -177,9 +177,9 @@ __device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
 // output is that value rounded, in every kernel. VOL picks the fence: a
 // volatile asm, which also bounds the compiler's scheduling regions, or a
 // plain one; the bits are the same. Measured on MI355X, the volatile one
-// schedules faster in the 8-wave GEMM tiles and the fused FFN kernel (C5
-// FFN 160 vs 170 us), the plain one in the 4-wave tiles (C2 ffn_in 15.5 vs
-// 17.5 us).
+// schedules faster in the 8-wave GEMM tiles (C4 ffn_in 263 vs 270 us), the
+// plain one everywhere else (C2 ffn_in 15.5 vs 17.5 us, the C5 fused FFN
+// 161 vs 164).
 template <bool VOL>
 __device__ __forceinline__ float gelu_erf(float x) {
     const float ax = fabsf(x);

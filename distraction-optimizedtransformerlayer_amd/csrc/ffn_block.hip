@@ -275,7 +275,7 @@ __global__ __launch_bounds__(NW * 64) void ffn_block_kernel(FfnArgs a) {
             const int c = nt * 32 + 8 * g + 4 * (lane >> 5);
             half4 hv;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) hv[e] = to_half(gelu_erf<true>(acc1[i][4 * g + e] + p_bin[c + e]));
+            for (int e = 0; e < 4; ++e) hv[e] = to_half(gelu_erf<false>(acc1[i][4 * g + e] + p_bin[c + e]));
             *reinterpret_cast<half4*>(sH + lr * PH + c) = hv;
         }
     }

@@ -183,7 +183,7 @@ __global__ __launch_bounds__(kWaves * 64) void ffn_ln_kernel(
             for (int e = 0; e < 4; ++e) {
                 float a = h[4 * grp + e];
                 a += bvs[e];
-                o[e] = static_cast<_Float16>(gelu_erf<true>(a));
+                o[e] = static_cast<_Float16>(gelu_erf<false>(a));
             }
             *reinterpret_cast<half4_t*>(hbuf + tr * 64 + ((4 * hc + grp) ^ L::swz(tr)) * 8 +
                                         4 * g.lg) = o;

@@ -328,7 +328,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
                     float v = acc[i][j][r];
                     if constexpr (SPLIT) v += acc2[i][j][r] * kLoUnscale;
                     v += bcol;
-                    if constexpr (ACT == DOTL_ACT_GELU) v = gelu_erf<true>(v);
+                    if constexpr (ACT == DOTL_ACT_GELU) v = gelu_erf<false>(v);
                     if constexpr (OUT_F16) {
                         static_cast<_Float16*>(C_)[row * N + col] = to_half(v);
                     } else {
