@@ -172,6 +172,70 @@ def test_declined_ffn_block_runs_unfused(monkeypatch):
     assert okernels._ffn_block(x, x, norm, ffn_in, ffn_out, norm) is None
 
 
+def test_fused_ffn_gate(monkeypatch):
+    """_ffn_ln_wanted: the one-kernel FFN exactly where the two GEMMs it
+    replaces would be the one-pass GELU GEMM (fp16 out) and the GEMM with the
+    LayerNorm epilogue, at d_model 256 and d_ff a multiple of 64 up to 2048."""
+    rows = config._LN_EPILOGUE_MIN_ROWS
+    x = torch.empty(rows, 256, dtype=torch.float16)
+    ffn_in, ffn_out = torch.nn.Linear(256, 1024), torch.nn.Linear(1024, 256)
+    assert okernels._ffn_ln_wanted(x, ffn_in, ffn_out)
+    assert not okernels._ffn_ln_wanted(x.float(), ffn_in, ffn_out)            # fp32 input
+    assert not okernels._ffn_ln_wanted(x[: rows - 1], ffn_in, ffn_out)         # too few rows
+    x128 = torch.empty(rows, 128, dtype=torch.float16)
+    assert not okernels._ffn_ln_wanted(x128, torch.nn.Linear(128, 512),
+                                       torch.nn.Linear(512, 128))              # d_model 128
+    for d_ff in (96, 4096):                                                    # d_ff % 64, > 2048
+        assert not okernels._ffn_ln_wanted(x, torch.nn.Linear(256, d_ff),
+                                           torch.nn.Linear(d_ff, 256))
+    assert not okernels._ffn_ln_wanted(x, torch.nn.Linear(256, 1024, bias=False), ffn_out)
+    for knob, value in (("FFN_LN", "off"), ("LN_EPILOGUE", "off"), ("LINEAR_GELU", "tf32"),
+                        ("GELU_FP16", "off")):
+        monkeypatch.setattr(config, knob, value)
+        assert not okernels._ffn_ln_wanted(x, ffn_in, ffn_out), knob
+        monkeypatch.undo()
+
+
+class _FfnKernels:
+    """Records the fused FFN call; declines (None) when asked to."""
+
+    def __init__(self, decline):
+        self.decline, self.calls = decline, []
+
+    def ffn_layernorm(self, x, *a, **k):
+        self.calls.append(k)
+        if self.decline:
+            return None
+        rows = x.shape[0]
+        return None, torch.full((rows, 256), 7.0)
+
+
+def test_fused_ffn_used_where_wanted(monkeypatch):
+    kx = _FfnKernels(decline=False)
+    monkeypatch.setattr(okernels, "_custom_kernels", lambda: kx)
+    monkeypatch.setattr(okernels, "_ffn_ln_wanted", lambda *a: True)
+    norm = omodel.MyLayerNorm(256)
+    x = torch.empty(4, 256, dtype=torch.float16)
+    h, out = okernels._ffn_norm(x, torch.nn.Linear(256, 1024), torch.nn.Linear(1024, 256),
+                                torch.zeros(4, 256), norm, "float", store_out=False)
+    assert h is None and bool((out == 7.0).all())
+    assert kx.calls and kx.calls[0]["normed"] == "float"
+
+
+def test_declined_fused_ffn_runs_the_two_gemms(monkeypatch):
+    kx = _FfnKernels(decline=True)
+    monkeypatch.setattr(okernels, "_custom_kernels", lambda: kx)
+    monkeypatch.setattr(okernels, "_ffn_ln_wanted", lambda *a: True)
+    seen = []
+    monkeypatch.setattr(okernels, "_linear_gelu", lambda x, lin, out_half=False: seen.append("gelu") or x)
+    monkeypatch.setattr(okernels, "_linear_norm",
+                        lambda hidden, lin, r, norm, kind, *a, **k: seen.append("norm") or ("h", "n"))
+    x = torch.empty(4, 256, dtype=torch.float16)
+    got = okernels._ffn_norm(x, torch.nn.Linear(256, 1024), torch.nn.Linear(1024, 256),
+                             torch.zeros(4, 256), omodel.MyLayerNorm(256), "float")
+    assert len(kx.calls) == 1 and seen == ["gelu", "norm"] and got == ("h", "n")
+
+
 def test_attention_without_the_library_raises(monkeypatch):
     import kernel_ext
 
